@@ -1,0 +1,24 @@
+"""flashloop_amd -- MI355X (gfx950) quantized cross-loop KV decode path of FlashLoop.
+
+Host side in Python over PyTorch-ROCm (device memory and streams); the work runs in
+hand-written HIP kernels of ``libflashloop_amd.so`` behind a C ABI
+(include/flashloop_amd.h).  There is no CPU fallback.
+"""
+
+from .cache import (  # noqa: F401
+    AttentionStep,
+    CrossLoopKVCache,
+    CrossLoopKVLayer,
+    LayerGeometry,
+    decode_attention_step,
+    packed_prefix_tokens,
+)
+
+__all__ = [
+    "AttentionStep",
+    "CrossLoopKVCache",
+    "CrossLoopKVLayer",
+    "LayerGeometry",
+    "decode_attention_step",
+    "packed_prefix_tokens",
+]

@@ -1,0 +1,446 @@
+"""Physical anchor-plus-residual cross-loop KV cache of one layer, in HBM.
+
+Mirrors ``CrossLoopKVLayer`` / ``CrossLoopKVCache`` (flashloop/cache.py:315-1950): the
+same streams (int4 anchor, int4 loop-2 residual, int4 loop-3/4 residuals at their
+active rows through rank maps), the same 64..127-token BF16 tail per loop, the same
+rollover of one 64-token group when the tail reaches 128 rows, and the same reader
+methods.  Differences, all deliberate:
+
+* batched: ``[B, H]`` sequences, each with its own prefix/tail length (the reference
+  is batch-one, flashloop/cache.py:270-271);
+* metadata is float32 and loop-3/4 K residuals are grouped per logical 64-token group
+  -- the arithmetic of flashloop_torch/kv_quantization.py:455-486, 531-650, so codes
+  and reconstructions match the torch reference bit for bit;
+* storage is token-major int4 rows (64 bytes per 128 channels) for every stream,
+  read by the HIP kernels in libflashloop_amd.so; there is no torch or CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+from . import kernels
+from ._lib import GROUP, HEAD_DIM, FlCacheView
+
+
+def packed_prefix_tokens(tokens: int, group: int = GROUP, residual: int = 64) -> int:
+    """Tokens held in packed streams (flashloop/cache.py:385-387)."""
+    return max(0, ((int(tokens) - residual) // group) * group)
+
+
+def _round_up(x: int, m: int) -> int:
+    return (int(x) + m - 1) // m * m
+
+
+@dataclass(frozen=True)
+class LayerGeometry:
+    batch: int
+    heads: int
+    token_capacity: int
+    tail_capacity: int
+    row_capacity: tuple[int, int, int, int]
+
+
+class CrossLoopKVLayer:
+    """One layer's packed recurrent cache for ``batch`` sequences of ``heads`` heads."""
+
+    residual_length = 64
+    group_size = GROUP
+
+    def __init__(self, geometry: LayerGeometry, device) -> None:
+        g = geometry
+        if g.token_capacity % GROUP:
+            raise ValueError("token_capacity must be a multiple of 64")
+        if g.tail_capacity < self.residual_length + GROUP:
+            raise ValueError("tail_capacity must hold 128 rows (residual + one group)")
+        self.geometry = g
+        self.device = torch.device(device)
+        rows = g.batch * g.heads
+        dev = self.device
+        self.key_codes = [torch.zeros(rows, g.row_capacity[s], HEAD_DIM // 2, dtype=torch.uint8, device=dev) for s in range(4)]
+        self.value_codes = [torch.zeros(rows, g.row_capacity[s], HEAD_DIM // 2, dtype=torch.uint8, device=dev) for s in range(4)]
+        self.key_meta = [torch.zeros(rows, g.token_capacity // GROUP, HEAD_DIM, 2, dtype=torch.float32, device=dev) for _ in range(4)]
+        self.value_meta = [torch.zeros(rows, g.row_capacity[s], 2, 2, dtype=torch.float32, device=dev) for s in range(4)]
+        self.rank = [torch.full((g.batch, g.token_capacity), -1, dtype=torch.int32, device=dev) for _ in range(2)]
+        self.tail_key = [torch.zeros(rows, g.tail_capacity, HEAD_DIM, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+        self.tail_value = [torch.zeros(rows, g.tail_capacity, HEAD_DIM, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+        # loop-3/4 activity of tail rows (flashloop/cache.py:_tail_active)
+        self.tail_active = [torch.zeros(g.batch, g.tail_capacity, dtype=torch.uint8, device=dev) for _ in range(2)]
+        self.packed_tokens = torch.zeros(g.batch, dtype=torch.int32, device=dev)
+        self.tail_tokens = torch.zeros(g.batch, dtype=torch.int32, device=dev)
+        self.late_rows = torch.zeros(2, g.batch, dtype=torch.int32, device=dev)  # rows used in streams 2/3
+        # host mirrors (no device sync on the decode path)
+        self.packed_host = [0] * g.batch
+        self.tail_host = [0] * g.batch
+        self.late_rows_host = [[0] * g.batch, [0] * g.batch]
+        self._view: FlCacheView | None = None
+        self.workspace = kernels.Workspace()
+
+    # ------------------------------------------------------------------ geometry
+    @property
+    def batch(self) -> int:
+        return self.geometry.batch
+
+    @property
+    def heads(self) -> int:
+        return self.geometry.heads
+
+    @property
+    def rows(self) -> int:
+        return self.batch * self.heads
+
+    @property
+    def quantized_tokens(self) -> int:
+        return max(self.packed_host)
+
+    @property
+    def tail_tokens_max(self) -> int:
+        return max(self.tail_host)
+
+    @property
+    def token_count(self) -> int:
+        return max(p + t for p, t in zip(self.packed_host, self.tail_host))
+
+    def view(self) -> FlCacheView:
+        if self._view is None:
+            g = self.geometry
+            v = FlCacheView()
+            v.batch, v.heads = g.batch, g.heads
+            v.token_capacity, v.tail_capacity = g.token_capacity, g.tail_capacity
+            for s in range(4):
+                v.row_capacity[s] = g.row_capacity[s]
+                v.key_codes[s] = self.key_codes[s].data_ptr()
+                v.key_meta[s] = self.key_meta[s].data_ptr()
+                v.value_codes[s] = self.value_codes[s].data_ptr()
+                v.value_meta[s] = self.value_meta[s].data_ptr()
+                v.tail_key[s] = self.tail_key[s].data_ptr()
+                v.tail_value[s] = self.tail_value[s].data_ptr()
+            v.rank[0], v.rank[1] = self.rank[0].data_ptr(), self.rank[1].data_ptr()
+            v.packed_tokens = self.packed_tokens.data_ptr()
+            v.tail_tokens = self.tail_tokens.data_ptr()
+            self._view = v
+        self._view.max_packed_tokens = self.quantized_tokens
+        self._view.max_tail_tokens = self.tail_tokens_max
+        return self._view
+
+    # ------------------------------------------------------------------ construction
+    @classmethod
+    def from_prefill(
+        cls,
+        keys: Sequence[torch.Tensor],
+        values: Sequence[torch.Tensor],
+        *,
+        mask_loop3: torch.Tensor | None = None,
+        mask_loop4: torch.Tensor | None = None,
+        lengths: Sequence[int] | None = None,
+        token_capacity: int | None = None,
+        recon: bool = False,
+    ) -> "CrossLoopKVLayer":
+        """Pack a prefill's four loop K/V ``[B, H, T, 128]`` bf16 (``CrossLoopKVLayer.from_prefill``,
+        flashloop/cache.py:752-817; codec of kv_quantization.py:531-650).
+
+        ``mask_loop3/4``: ``[B, T]`` bool rows recomputed in loops 3/4 (None = all rows);
+        ``lengths``: per-sequence token counts for ragged batches (rows beyond are padding);
+        ``token_capacity``: packed-prefix capacity (room for decode rollover).
+        With ``recon=True`` the reconstructed prefixes R_r are returned as
+        ``layer.recon_keys/recon_values`` (bf16 ``[B*H, T, 128]``) for audits.
+        """
+        if len(keys) != 4 or len(values) != 4:
+            raise ValueError("exactly four loop K/V tensors are required")
+        b, h, t, c = keys[0].shape
+        if c != HEAD_DIM:
+            raise ValueError("head_dim must be 128")
+        for x in (*keys, *values):
+            if tuple(x.shape) != (b, h, t, c) or x.dtype != torch.bfloat16 or not x.is_cuda:
+                raise ValueError("loop K/V must be bf16 device tensors of one shape [B, H, T, 128]")
+        lengths = [t] * b if lengths is None else [int(x) for x in lengths]
+        if len(lengths) != b or any(x <= 0 or x > t for x in lengths):
+            raise ValueError("lengths must give 1..T tokens per sequence")
+        dev = keys[0].device
+        masks = []
+        for m in (mask_loop3, mask_loop4):
+            if m is None:
+                masks.append(torch.ones(b, t, dtype=torch.bool, device=dev))
+            else:
+                if tuple(m.shape) != (b, t):
+                    raise ValueError("prefill masks must have shape [B, T]")
+                masks.append(m.to(device=dev, dtype=torch.bool))
+        if not bool(torch.all(~masks[1] | masks[0]).item()):
+            raise ValueError("Loop-4 overrides must be nested in Loop-3 overrides")
+        tp = [packed_prefix_tokens(x) for x in lengths]
+        tp_max = max(tp)
+        cap = _round_up(max(token_capacity or 0, tp_max, GROUP), GROUP)
+        # loop-3/4 compact rows of the packed prefix: rank = running count of active rows
+        pos = torch.arange(t, device=dev)
+        tp_t = torch.tensor(tp, device=dev)
+        prefix = pos[None, :] < tp_t[:, None]
+        late_counts = []
+        ranks = []
+        for m in masks:
+            act = m & prefix
+            r = torch.cumsum(act.to(torch.int32), dim=1) - 1
+            r = torch.where(act, r, torch.full_like(r, -1)).to(torch.int32)
+            ranks.append(r)
+            late_counts.append([int(x) for x in act.sum(dim=1).tolist()])
+        growth = cap - min(tp)  # every future decode token is active in every loop
+        row_cap = (cap, cap, max(late_counts[0]) + growth, max(late_counts[1]) + growth)
+        layer = cls(LayerGeometry(b, h, cap, 2 * GROUP, row_cap), dev)
+        for s in range(2):
+            layer.rank[s][:, : min(t, cap)] = ranks[s][:, : min(t, cap)]
+            layer.late_rows_host[s] = late_counts[s]
+            layer.late_rows[s] = torch.tensor(late_counts[s], dtype=torch.int32, device=dev)
+        layer.packed_host = list(tp)
+        layer.tail_host = [x - p for x, p in zip(lengths, tp)]
+        layer.packed_tokens.copy_(torch.tensor(tp, dtype=torch.int32))
+        layer.tail_tokens.copy_(torch.tensor(layer.tail_host, dtype=torch.int32))
+        if tp_max:
+            src_k = [x.reshape(b * h, t, c) for x in keys]
+            src_v = [x.reshape(b * h, t, c) for x in values]
+            mk = [m.to(torch.uint8).contiguous() for m in masks]
+            rk = rv = None
+            if recon:
+                rk = [torch.zeros(b * h, t, c, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+                rv = [torch.zeros(b * h, t, c, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+            kernels.pack_kv_groups(
+                layer.view(), 4, [x.contiguous() for x in src_k], [x.contiguous() for x in src_v],
+                src_bh_stride=t, src_row_offset=0,
+                dst_group0=torch.zeros(b, dtype=torch.int32, device=dev), n_groups=tp_max // GROUP,
+                masks=mk, mask_stride=t, recon_keys=rk, recon_values=rv,
+            )
+            if recon:
+                layer.recon_keys, layer.recon_values = rk, rv
+        # BF16 tails (flashloop/cache.py:806-812)
+        for bi, (p, n) in enumerate(zip(tp, lengths)):
+            rows = slice(bi * h, (bi + 1) * h)
+            for r in range(4):
+                layer.tail_key[r][rows, : n - p] = keys[r][bi, :, p:n]
+                layer.tail_value[r][rows, : n - p] = values[r][bi, :, p:n]
+            for s in range(2):
+                layer.tail_active[s][bi, : n - p] = masks[s][bi, p:n].to(torch.uint8)
+        return layer
+
+    # ------------------------------------------------------------------ readers
+    def logits_capacity(self) -> int:
+        return self.token_count + 1
+
+    def dense_source_attention(self, loop: int, *, query, current_key, current_value, scaling: float,
+                               return_logits: bool):
+        """``CrossLoopKVLayer.dense_source_attention`` (flashloop/cache.py:1644-1756).
+
+        Returns ``(out f32 [B,H,1,128], logits f32 [B,H,1,T+1] or None)``; for ragged
+        batches logits rows are valid up to each sequence's own ``T+1``."""
+        out, logits = kernels.fused_dense_source_attention(
+            self.view(), int(loop), query, current_key, current_value, scaling, return_logits=return_logits,
+            logits_capacity=self.logits_capacity(), device=self.device, workspace=self.workspace,
+        )
+        out = out.view(self.batch, self.heads, 1, HEAD_DIM)
+        if logits is not None:
+            logits = logits.view(self.batch, self.heads, 1, -1)
+        return out, logits
+
+    def key_counts(self) -> torch.Tensor:
+        """Keys per sequence including the current token: packed + tail + 1 (device)."""
+        return self.packed_tokens + self.tail_tokens + 1
+
+    def select_decode_keys(self, logits: torch.Tensor, fraction: float):
+        """Loop-2 key selection (flashloop/engine.py:438-498) on the dense reader's logits.
+        Returns ``(indices, valid, mass [B,H,1,1], selected_weights, counts)``."""
+        cap = kernels.decode_capacity(self.token_count + 1, fraction)
+        idx, valid, mass, w, counts = kernels.decode_topk(
+            logits.reshape(self.rows, -1), self.key_counts(), fraction, cap, rows_per_count=self.heads
+        )
+        shape = (self.batch, self.heads, cap)
+        return idx.view(shape), valid.view(shape), mass.view(self.batch, self.heads, 1, 1), w.view(shape), counts
+
+    def pv(self, loop: int, weights, indices, valid, current_value):
+        """``_selected_value_aggregate`` (flashloop/engine.py:346-371): sum of selected V rows
+        of loop ``loop`` weighted by ``weights``; the current token reads ``current_value``."""
+        out = kernels.fused_cross_loop_pv(self.view(), int(loop), indices, valid, weights, current_value,
+                                          device=self.device, workspace=self.workspace)
+        return out.view(self.batch, self.heads, 1, HEAD_DIM)
+
+    def cached_mass_sparse_attention_delta(self, loop: int, *, query, current_key, current_value, indices, valid,
+                                           source_selected_output, global_mass, scaling: float):
+        """``CrossLoopKVLayer.cached_mass_sparse_attention_delta`` (flashloop/cache.py:1517-1617)."""
+        if int(loop) not in (2, 3):
+            raise ValueError("cached-mass sparse attention is only valid for Loop 3/4")
+        out = kernels.fused_sparse_attention_delta(
+            self.view(), int(loop), query, current_key, current_value, indices, valid, source_selected_output,
+            global_mass, scaling, device=self.device, workspace=self.workspace,
+        )
+        return out.view(self.batch, self.heads, 1, HEAD_DIM)
+
+    # ------------------------------------------------------------------ decode append
+    def append_decode_token(self, keys: Sequence[torch.Tensor], values: Sequence[torch.Tensor]) -> None:
+        """``append_decode_token`` (flashloop/cache.py:1758-1776): write the step's four loop
+        K/V rows (``[B,H,1,128]``) into the tails; roll a group out when a tail reaches 128."""
+        if len(keys) != 4 or len(values) != 4:
+            raise ValueError("exactly four loop K/V tensors are required")
+        b, h = self.batch, self.heads
+        cap = self.geometry.tail_capacity
+        if any(t >= cap for t in self.tail_host):
+            raise RuntimeError("tail is full; rollover did not run")
+        uniform = len(set(self.tail_host)) == 1
+        for r in range(4):
+            k = keys[r].reshape(b * h, HEAD_DIM)
+            v = values[r].reshape(b * h, HEAD_DIM)
+            if uniform:
+                pos = self.tail_host[0]
+                self.tail_key[r][:, pos] = k
+                self.tail_value[r][:, pos] = v
+            else:
+                rows = torch.arange(b * h, device=self.device)
+                pos = torch.tensor(self.tail_host, device=self.device).repeat_interleave(h)
+                self.tail_key[r][rows, pos] = k
+                self.tail_value[r][rows, pos] = v
+        for s in range(2):
+            for bi in range(b):
+                self.tail_active[s][bi, self.tail_host[bi]] = 1
+        self.tail_host = [x + 1 for x in self.tail_host]
+        self.tail_tokens += 1
+        if any(x >= self.residual_length + GROUP for x in self.tail_host):
+            self._roll_groups()
+
+    def _roll_groups(self) -> None:
+        """``_roll_one_group`` (flashloop/cache.py:1778-1838) for every sequence whose tail
+        holds residual+group rows: pack tail rows [0, 64) as prefix group Tp/64, then shift
+        the tail down by 64.  O(group): the prefix is never re-read."""
+        b, h = self.batch, self.heads
+        roll = [x >= self.residual_length + GROUP for x in self.tail_host]
+        g0 = [self.packed_host[i] // GROUP if roll[i] else -1 for i in range(b)]
+        for i in range(b):
+            if roll[i] and self.packed_host[i] + GROUP > self.geometry.token_capacity:
+                raise RuntimeError("packed prefix capacity exhausted; allocate a larger token_capacity")
+        # rank maps of the new group's rows (active rows continue the compact numbering)
+        for s in range(2):
+            for i in range(b):
+                if not roll[i]:
+                    continue
+                act = self.tail_active[s][i, :GROUP].bool()
+                n_act = int(act.sum().item())
+                base = self.late_rows_host[s][i]
+                if base + n_act > self.geometry.row_capacity[s + 2]:
+                    raise RuntimeError("loop-3/4 row capacity exhausted")
+                r = torch.cumsum(act.to(torch.int32), 0) - 1 + base
+                r = torch.where(act, r, torch.full_like(r, -1)).to(torch.int32)
+                p = self.packed_host[i]
+                self.rank[s][i, p : p + GROUP] = r
+                self.late_rows_host[s][i] = base + n_act
+        dst = torch.tensor(g0, dtype=torch.int32, device=self.device)
+        kernels.pack_kv_groups(
+            self.view(), 4, self.tail_key, self.tail_value, src_bh_stride=self.geometry.tail_capacity,
+            src_row_offset=0, dst_group0=dst, n_groups=1, masks=self.tail_active,
+            mask_stride=self.geometry.tail_capacity,
+        )
+        for i in range(b):
+            if not roll[i]:
+                continue
+            rows = slice(i * h, (i + 1) * h)
+            n = self.tail_host[i] - GROUP
+            for tensor in (*self.tail_key, *self.tail_value):
+                tensor[rows, :n] = tensor[rows, GROUP : GROUP + n].clone()
+            for act in self.tail_active:
+                act[i, :n] = act[i, GROUP : GROUP + n].clone()
+                act[i, n:] = 0
+            self.packed_host[i] += GROUP
+            self.tail_host[i] = n
+        self.packed_tokens.copy_(torch.tensor(self.packed_host, dtype=torch.int32))
+        self.tail_tokens.copy_(torch.tensor(self.tail_host, dtype=torch.int32))
+        self.late_rows.copy_(torch.tensor(self.late_rows_host, dtype=torch.int32))
+
+    # ------------------------------------------------------------------ accounting
+    @property
+    def storage_bytes(self) -> int:
+        """Bytes of the used part of every buffer (cf. flashloop/cache.py:1084-1112)."""
+        b, h = self.batch, self.heads
+        tot = 0
+        for i in range(b):
+            p = self.packed_host[i]
+            rows = [p, p, self.late_rows_host[0][i], self.late_rows_host[1][i]]
+            for s in range(4):
+                tot += h * rows[s] * (64 + 64 + 16)  # K/V codes + V meta
+                tot += h * (p // GROUP) * HEAD_DIM * 8  # K meta
+            tot += 4 * 2 * h * self.tail_host[i] * HEAD_DIM * 2
+            tot += 2 * p * 4  # rank maps
+        return tot
+
+    @property
+    def dense_bf16_bytes(self) -> int:
+        return 4 * 2 * self.heads * sum(p + t for p, t in zip(self.packed_host, self.tail_host)) * HEAD_DIM * 2
+
+
+class CrossLoopKVCache:
+    """Layer-indexed owner of physical cross-loop KV storage (flashloop/cache.py:1841-1950)."""
+
+    def __init__(self, *, num_layers: int) -> None:
+        if int(num_layers) <= 0:
+            raise ValueError("num_layers must be positive")
+        self.layers: list[CrossLoopKVLayer | None] = [None] * int(num_layers)
+
+    def set_layer(self, layer_index: int, layer: CrossLoopKVLayer) -> None:
+        if layer_index not in range(len(self.layers)):
+            raise IndexError("layer index is outside the cache")
+        if self.layers[layer_index] is not None:
+            raise RuntimeError("physical cache layer is already installed")
+        self.layers[layer_index] = layer
+
+    def _require_layer(self, layer_index: int) -> CrossLoopKVLayer:
+        if layer_index not in range(len(self.layers)):
+            raise IndexError("layer index is outside the cache")
+        layer = self.layers[layer_index]
+        if layer is None:
+            raise RuntimeError("physical cache layer has not been installed")
+        return layer
+
+    def dense_source_attention(self, layer_index: int, loop: int, **kwargs):
+        return self._require_layer(layer_index).dense_source_attention(loop, **kwargs)
+
+    def cached_mass_sparse_attention_delta(self, layer_index: int, loop: int, **kwargs):
+        return self._require_layer(layer_index).cached_mass_sparse_attention_delta(loop, **kwargs)
+
+    def pv(self, layer_index: int, loop: int, weights, indices, valid, current_value):
+        return self._require_layer(layer_index).pv(loop, weights, indices, valid, current_value)
+
+    @property
+    def storage_bytes(self) -> int:
+        return sum(layer.storage_bytes for layer in self.layers if layer is not None)
+
+
+@dataclass
+class AttentionStep:
+    out0: torch.Tensor
+    out1: torch.Tensor
+    logits1: torch.Tensor
+    indices: torch.Tensor
+    valid: torch.Tensor
+    mass: torch.Tensor
+    selected_weights: torch.Tensor
+    counts: torch.Tensor
+    selected_output: torch.Tensor
+    delta2: torch.Tensor
+    delta3: torch.Tensor
+
+
+def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scaling: float,
+                          fraction: float = 0.10) -> AttentionStep:
+    """One layer's decode attention over four loops (flashloop/engine.py:422-531, before
+    ``o_proj``): dense loops 1-2 (loop 2 with logits), loop-2 key selection and selected
+    aggregate, then the cached-mass deltas of loops 3-4.  ``queries/keys/values``: four
+    bf16 ``[B,H,1,128]`` (the current token of each loop)."""
+    out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=keys[0], current_value=values[0],
+                                           scaling=scaling, return_logits=False)
+    out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=keys[1], current_value=values[1],
+                                                scaling=scaling, return_logits=True)
+    idx, valid, mass, w, counts = layer.select_decode_keys(logits, fraction)
+    so = layer.pv(1, w, idx, valid, values[1])
+    d2 = layer.cached_mass_sparse_attention_delta(2, query=queries[2], current_key=keys[2], current_value=values[2],
+                                                  indices=idx, valid=valid, source_selected_output=so,
+                                                  global_mass=mass, scaling=scaling)
+    d3 = layer.cached_mass_sparse_attention_delta(3, query=queries[3], current_key=keys[3], current_value=values[3],
+                                                  indices=idx, valid=valid, source_selected_output=so,
+                                                  global_mass=mass, scaling=scaling)
+    return AttentionStep(out0, out1, logits, idx, valid, mass, w, counts, so, d2, d3)

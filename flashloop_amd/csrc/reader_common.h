@@ -1,0 +1,136 @@
+// Helpers shared by the dense and the gather (sparse / selected) decode readers.
+#pragma once
+
+#include "fl_common.h"
+
+namespace fl {
+namespace reader {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kPartial = kDim + 2;  // m, l, acc[128]
+
+
+__device__ __forceinline__ float ubyte0(uint32_t w) { return static_cast<float>(w & 0xFFu); }
+__device__ __forceinline__ float ubyte1(uint32_t w) { return static_cast<float>((w >> 8) & 0xFFu); }
+__device__ __forceinline__ float ubyte2(uint32_t w) { return static_cast<float>((w >> 16) & 0xFFu); }
+__device__ __forceinline__ float ubyte3(uint32_t w) { return static_cast<float>(w >> 24); }
+
+// 8 nibbles of word w: bytes hold (even channel lo, odd channel hi).
+// acc += sum_e qe[e]*lo_e + qo[e]*hi_e, with qo pre-divided by 16 because the high
+// nibbles are converted in place (value 16*code).
+__device__ __forceinline__ float dot8(uint32_t w, const float* qe, const float* qo, float acc) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;
+  const uint32_t hi = w & 0xF0F0F0F0u;
+  acc = fmaf(qe[0], ubyte0(lo), acc);
+  acc = fmaf(qe[1], ubyte1(lo), acc);
+  acc = fmaf(qe[2], ubyte2(lo), acc);
+  acc = fmaf(qe[3], ubyte3(lo), acc);
+  acc = fmaf(qo[0], ubyte0(hi), acc);
+  acc = fmaf(qo[1], ubyte1(hi), acc);
+  acc = fmaf(qo[2], ubyte2(hi), acc);
+  acc = fmaf(qo[3], ubyte3(hi), acc);
+  return acc;
+}
+
+// acc[8 channels of word] += w_even*code (lo) and w_odd16*(16*code) (hi)
+__device__ __forceinline__ void axpy8(uint32_t w, float we, float wo, float* acc) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;
+  const uint32_t hi = w & 0xF0F0F0F0u;
+  acc[0] = fmaf(we, ubyte0(lo), acc[0]);
+  acc[2] = fmaf(we, ubyte1(lo), acc[2]);
+  acc[4] = fmaf(we, ubyte2(lo), acc[4]);
+  acc[6] = fmaf(we, ubyte3(lo), acc[6]);
+  acc[1] = fmaf(wo, ubyte0(hi), acc[1]);
+  acc[3] = fmaf(wo, ubyte1(hi), acc[3]);
+  acc[5] = fmaf(wo, ubyte2(hi), acc[5]);
+  acc[7] = fmaf(wo, ubyte3(hi), acc[7]);
+}
+
+struct QuadState {
+  float m, l, mu;
+  float acc[32];
+};
+
+__device__ __forceinline__ void online_update(QuadState& st, const float* lg, float* p, int n) {
+  float mloc = st.m;
+  for (int i = 0; i < n; ++i) mloc = fmaxf(mloc, lg[i]);
+  if (mloc == -INFINITY) {  // nothing valid yet
+    for (int i = 0; i < n; ++i) p[i] = 0.0f;
+    return;
+  }
+  const float alpha = fast_exp2((st.m - mloc) * kLog2e);
+  float ps = 0.0f;
+  for (int i = 0; i < n; ++i) {
+    p[i] = fast_exp2((lg[i] - mloc) * kLog2e);
+    ps += p[i];
+  }
+  st.l = st.l * alpha + ps;
+  st.mu *= alpha;
+#pragma unroll
+  for (int c = 0; c < 32; ++c) st.acc[c] *= alpha;
+  st.m = mloc;
+}
+
+// Merge the 64 quad states of the workgroup and write one partial (m, l, acc[128]).
+__device__ void write_partial(QuadState& st, float* part, float (*comb)[16][kDim], float* lsh, float* msh) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, quarter = lane & 3, row = lane >> 2;
+  const float mw = wave_max(st.m);
+  if (lane == 0) msh[wave] = mw;
+  __syncthreads();
+  float M = msh[0];
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, msh[w]);
+  const float f = (st.m == -INFINITY) ? 0.0f : fast_exp2((st.m - M) * kLog2e);
+#pragma unroll
+  for (int c = 0; c < 32; ++c) comb[wave][row][32 * quarter + c] = (st.acc[c] + st.mu) * f;
+  if (quarter == 0) lsh[wave * 16 + row] = st.l * f;
+  __syncthreads();
+  if (tid < kDim) {
+    float s = 0.0f;
+    for (int w = 0; w < kWaves; ++w)
+      for (int r = 0; r < 16; ++r) s += comb[w][r][tid];
+    part[2 + tid] = s;
+  } else if (tid == kDim) {
+    float s = 0.0f;
+    for (int i = 0; i < kWaves * 16; ++i) s += lsh[i];
+    part[0] = M;
+    part[1] = s;
+  }
+}
+
+enum MergeMode { kMergeSoftmax = 0, kMergeMassDelta = 1, kMergeSum = 2 };
+
+// Combine a row's split partials (m, l, acc[128]).
+//   kMergeSoftmax:   out = sum_i e^{m_i-M} acc_i / sum_i e^{m_i-M} l_i
+//   kMergeMassDelta: out = mass * (softmax merge - src)
+//   kMergeSum:       out = sum_i acc_i
+__global__ __launch_bounds__(kDim) void merge_partials_kernel(const float* ws, int nparts, float* out, int mode,
+                                                              const float* mass, const float* src) {
+  const int bh = blockIdx.x, c = threadIdx.x;
+  const float* p = ws + static_cast<int64_t>(bh) * nparts * kPartial;
+  float res;
+  if (mode == kMergeSum) {
+    float acc = 0.0f;
+    for (int i = 0; i < nparts; ++i) acc += p[i * kPartial + 2 + c];
+    res = acc;
+  } else {
+    float M = -INFINITY;
+    for (int i = 0; i < nparts; ++i) M = fmaxf(M, p[i * kPartial]);
+    float L = 0.0f, acc = 0.0f;
+    for (int i = 0; i < nparts; ++i) {
+      const float m = p[i * kPartial];
+      if (m == -INFINITY) continue;
+      const float f = fast_exp2((m - M) * kLog2e);
+      L = fmaf(p[i * kPartial + 1], f, L);
+      acc = fmaf(p[i * kPartial + 2 + c], f, acc);
+    }
+    res = acc / L;
+    if (mode == kMergeMassDelta) res = mass[bh] * (res - src[static_cast<int64_t>(bh) * kDim + c]);
+  }
+  out[static_cast<int64_t>(bh) * kDim + c] = res;
+}
+
+}  // namespace
+}  // namespace reader
+}  // namespace fl

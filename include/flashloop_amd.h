@@ -1,0 +1,238 @@
+/*
+ * flashloop_amd -- C ABI of the MI355X (gfx950) quantized cross-loop KV decode path.
+ *
+ * Every entry point is a plain C function over device pointers and sizes.  It is
+ * asynchronous on the HIP stream passed as `stream` (a hipStream_t, NULL = the null
+ * stream), allocates nothing (outputs and workspaces belong to the caller), throws
+ * nothing, and returns FL_OK (0) or a negative FL_E* code; fl_last_error() then holds
+ * a message for the calling thread.  Argument checks that need no device access
+ * happen before any launch, so an error return means nothing was enqueued.
+ *
+ * The reference boundary these replace is the pybind11 module `flashloop_kivi_gemv`
+ * (flashloop/csrc/kivi_outer_gemv_binding.cpp:5-34, declared in
+ * flashloop/csrc/kivi_outer_gemv_cuda.h:6-120) plus the Triton packing kernels it
+ * relies on (flashloop/kivi_backend.py:162-256) and the torch glue around
+ * selection and token-sparse updates (flashloop/engine.py:84-109, 276-333,
+ * flashloop/prefill.py:158-237).  Each declaration below cites the function it
+ * replaces.
+ *
+ * Fixed geometry (flashloop/config.py:18-65, 92-134): head_dim 128, 4-bit codes,
+ * group 64, multi-head attention (query heads == KV heads), at most 4 loops.
+ */
+#ifndef FLASHLOOP_AMD_H
+#define FLASHLOOP_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FL_OK 0
+#define FL_E_INVALID -1 /* bad argument: null pointer, shape, range */
+#define FL_E_LAUNCH -2  /* a HIP launch or runtime call failed */
+#define FL_E_CAPACITY -3 /* a size exceeds what the kernel or a buffer supports */
+
+#define FL_HEAD_DIM 128
+#define FL_GROUP 64
+#define FL_MAX_LOOPS 4
+
+/*
+ * One layer's packed cross-loop KV cache for a batch of sequences, in HBM.
+ *
+ * Rows are addressed per (batch, head) pair `bh = b * heads + h`.  Stream s holds
+ * loop s+1: s = 0 is the int4 anchor, s >= 1 the int4 residual against the previous
+ * loop's reconstruction.  Streams 0 and 1 are dense over the packed prefix; streams 2
+ * and 3 store only the rows active in loops 3 and 4, at compact rows given by the
+ * rank maps.  Code rows are token-major: byte j of a 64-byte row holds channel 2j in
+ * its low nibble and channel 2j+1 in its high nibble (flashloop/packing.py:1-6, 49-54).
+ *
+ *   key_codes[s]   u8  [B*H, row_capacity[s], 64]
+ *   key_meta[s]    f32 [B*H, token_capacity/64, 128, 2]  (scale, min) per channel per
+ *                      logical 64-token group (groups of streams 2/3 are logical too)
+ *   value_codes[s] u8  [B*H, row_capacity[s], 64]
+ *   value_meta[s]  f32 [B*H, row_capacity[s], 2, 2]      (scale, min) per 64-channel half
+ *   rank[0], rank[1] i32 [B, token_capacity]  compact row of stream 2 / 3, or -1
+ *   tail_key[r], tail_value[r] bf16 [B*H, tail_capacity, 128]  loop r's BF16 tail
+ *   packed_tokens, tail_tokens  i32 [B] (device)  per-sequence prefix / tail lengths
+ *
+ * Metadata is float32 so that the stored scale/min are bit-identical to the reference
+ * codec (flashloop_torch/kv_quantization.py:395-414) and the residual chain stays exact.
+ */
+typedef struct fl_cache_view {
+  int32_t batch;
+  int32_t heads;
+  int32_t token_capacity;  /* multiple of 64 */
+  int32_t tail_capacity;
+  int32_t row_capacity[4]; /* row_capacity[0] == row_capacity[1] == token_capacity */
+  uint8_t* key_codes[4];
+  float* key_meta[4];
+  uint8_t* value_codes[4];
+  float* value_meta[4];
+  int32_t* rank[2];
+  uint16_t* tail_key[4];
+  uint16_t* tail_value[4];
+  const int32_t* packed_tokens;
+  const int32_t* tail_tokens;
+  int32_t max_packed_tokens; /* host-side upper bound of packed_tokens (grid sizing) */
+  int32_t max_tail_tokens;   /* host-side upper bound of tail_tokens */
+} fl_cache_view;
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* fl_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int32_t fl_abi_version(void);
+
+/*
+ * J1 -- quantize and pack 64-token temporal groups through the residual chain.
+ *
+ * Replaces the Triton packers `_triton_pack_kivi` / `pack_kivi_k_per_channel` /
+ * `pack_kivi_v_per_token` (flashloop/kivi_backend.py:162-256, 404-475) as driven by
+ * `CrossLoopKVLayerBuilder.from_loop1/add_loop2/finalize` (flashloop/cache.py:342-625)
+ * and `_roll_one_group` (flashloop/cache.py:1778-1838), with the arithmetic of
+ * `encode_temporal_group` (flashloop_torch/kv_quantization.py:531-650).
+ *
+ * For each batch b with dst_group0[b] >= 0 and each j < n_groups, the group of 64
+ * source rows starting at `src_row_offset + 64*j` of every (b,h) is encoded into
+ * logical group `dst_group0[b] + j` of `view` for loops 0..loops-1:
+ *   R_0 = fq(L_0);  R_r = R_{r-1} + fq(L_r - R_{r-1}) over the rows active in loop r.
+ * Sources: bf16 rows of 128 channels, (b,h) block stride `src_bh_stride` rows.
+ * masks[0], masks[1]: u8 [B, mask_stride] activity of loops 3/4 by source row, or NULL
+ * for all rows; an active row must have rank >= 0 in the matching rank map.
+ * recon_keys/recon_values (optional, per loop, same layout as the sources) receive
+ * R_r as bf16.
+ */
+int32_t fl_pack_kv_groups(const fl_cache_view* view, int32_t loops,
+                          const uint16_t* const* src_keys, const uint16_t* const* src_values,
+                          int64_t src_bh_stride, int32_t src_row_offset,
+                          const uint8_t* const* masks, int64_t mask_stride,
+                          const int32_t* dst_group0, int32_t n_groups,
+                          uint16_t* const* recon_keys, uint16_t* const* recon_values,
+                          void* stream);
+
+/*
+ * J2 -- fused dense decode reader: dequantize, rebuild loop `loop`, q.K^T, online
+ * softmax, P.V, split over tokens and merged.
+ *
+ * Replaces `dense_source_attention_cuda` (flashloop/csrc/kivi_outer_gemv_cuda.h:98-120,
+ * kernels at flashloop/csrc/kivi_outer_gemv_cuda.cu:722-1013, 1914-2076) as called by
+ * `CrossLoopKVLayer.dense_source_attention` (flashloop/cache.py:1644-1756).  Keys:
+ * packed prefix (streams 0..loop, streams 2/3 through the rank maps), then loop
+ * `loop`'s tail, then the current token.  q, k_cur, v_cur: bf16 [B*H, 128].
+ * out: f32 [B*H, 128].  logits (optional): f32, row bh at `logits + bh*logits_stride`,
+ * holding scaling*q.k for the packed_tokens[b] + tail_tokens[b] + 1 keys.
+ * `loop` in 0..3 (the reference kernel supports 0..1; 2..3 serve
+ * enable_sparse_decode=False, flashloop/engine.py:422).
+ * workspace: fl_decode_attn_dense_workspace() bytes, any content.
+ */
+size_t fl_decode_attn_dense_workspace(const fl_cache_view* view);
+int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
+                             const uint16_t* q, const uint16_t* k_cur, const uint16_t* v_cur,
+                             float scaling, float* out, float* logits, int64_t logits_stride,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * J3 -- decode top-k key selection for sparse late-loop decode.
+ *
+ * Replaces the torch sequence softmax -> topk -> sort -> gather -> `_pad_decode_indices`
+ * -> mass -> normalise of `FlashLoopEngine.decode` (flashloop/engine.py:438-498,
+ * 84-109) and `select_decode_keys` (flashloop/selection.py:72-88).  Row r holds
+ * n_keys[r / heads_per_count] scores at `scores + r*scores_stride` (the dense reader's
+ * logits).  It selects k = min(n, max(1, ceil(n*fraction))) keys, ranked by score,
+ * ties to the lower index, and writes them ascending:
+ *   indices i32 [rows, capacity] (0-padded), valid u8 [rows, capacity],
+ *   mass f32 [rows] = sum of the selected softmax weights,
+ *   weights f32 [rows, capacity] = softmax weight / mass (0 where invalid).
+ * `capacity` must be >= k for every row (the engine uses (k/64+1)*64).
+ * counts (optional) i32 [rows] receives k.
+ */
+int32_t fl_decode_topk(const float* scores, int64_t scores_stride, int32_t rows,
+                       const int32_t* n_keys, int32_t rows_per_count, double fraction,
+                       int32_t capacity, int32_t* indices, uint8_t* valid, float* mass,
+                       float* weights, int32_t* counts, void* stream);
+
+/*
+ * J2 (sparse) -- weighted sum of selected V rows of loop `loop`.
+ *
+ * Replaces `pv_cross_loop_cuda` (flashloop/csrc/kivi_outer_gemv_cuda.h:54-67, kernel
+ * flashloop/csrc/kivi_outer_gemv_cuda.cu:296-394) as used by
+ * `FlashLoopEngine._selected_value_aggregate` (flashloop/engine.py:346-371):
+ *   out[bh] = sum_j valid*weights[bh,j] * V_loop[indices[bh,j]],
+ * where index packed_tokens[b]+tail_tokens[b] is the current token (v_cur).
+ * indices/valid/weights: [B*H, capacity].  out f32 [B*H, 128].
+ */
+size_t fl_decode_selected_workspace(const fl_cache_view* view, int32_t capacity);
+int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop, const int32_t* indices,
+                              const uint8_t* valid, const float* weights, int32_t capacity,
+                              const uint16_t* v_cur, float* out,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * J2 (sparse) -- cached-mass late-loop attention correction for loops 3/4.
+ *
+ * Replaces `sparse_attention_delta_cuda` (flashloop/csrc/kivi_outer_gemv_cuda.h:69-96,
+ * kernels flashloop/csrc/kivi_outer_gemv_cuda.cu:1015-1331) as called by
+ * `CrossLoopKVLayer.cached_mass_sparse_attention_delta` (flashloop/cache.py:1517-1617):
+ *   delta = mass * (softmax_S(scaling*q.K_loop[S]) . V_loop[S] - source_output)
+ * over the valid selected indices S (the current token handled as in
+ * fl_decode_selected_pv, with k_cur/v_cur).  source_output f32 [B*H,128],
+ * mass f32 [B*H], out f32 [B*H,128].
+ */
+int32_t fl_decode_attn_sparse_delta(const fl_cache_view* view, int32_t loop,
+                                    const uint16_t* q, const uint16_t* k_cur,
+                                    const uint16_t* v_cur, const int32_t* indices,
+                                    const uint8_t* valid, int32_t capacity,
+                                    const float* source_output, const float* mass,
+                                    float scaling, float* out,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * J4 -- token-sparse update row movement.
+ *
+ * fl_gather_rows replaces the `index_select` of active rows (flashloop/prefill.py:158,
+ * flashloop/engine.py:284-316); fl_scatter_rows replaces `index_copy_`
+ * (flashloop/prefill.py:193-194, 237).  A tensor is seen as [outer, rows, row_bytes]
+ * with the given strides (bytes):
+ *   gather: dst[o, i] = src[o, index[i]]   for i < n_index
+ *   scatter: dst[o, index[i]] = src[o, i]  for i < n_index  (indices distinct)
+ * row_bytes and all strides must be multiples of 4; indices are bounds-checked on the
+ * device (an out-of-range index skips its row and sets *error_flag to 1 if given).
+ */
+int32_t fl_gather_rows(const void* src, int64_t src_outer_stride, int64_t src_row_stride,
+                       int64_t src_rows, void* dst, int64_t dst_outer_stride,
+                       int64_t dst_row_stride, int64_t outer, int64_t row_bytes,
+                       const int32_t* index, int64_t n_index, int32_t* error_flag,
+                       void* stream);
+int32_t fl_scatter_rows(const void* src, int64_t src_outer_stride, int64_t src_row_stride,
+                        void* dst, int64_t dst_outer_stride, int64_t dst_row_stride,
+                        int64_t dst_rows, int64_t outer, int64_t row_bytes,
+                        const int32_t* index, int64_t n_index, int32_t* error_flag,
+                        void* stream);
+
+/*
+ * J4 -- loop-boundary token score and selection.
+ *
+ * fl_hidden_delta_score replaces `_hidden_delta_score` (flashloop/engine.py:78-81):
+ *   score[r] = ||cur[r] - prev[r]|| / max(||cur[r]||, 1e-12) over bf16 rows of `dim`.
+ * fl_select_tokens replaces `select_prefill_tokens` (flashloop/selection.py:26-69):
+ * per batch row of `tokens` scores, budget = max(1, ceil(tokens*fraction)); among the
+ * eligible tokens (eligible u8 [B, tokens] or NULL) minus the forced last token, the
+ * top (count - forced) by score (ties: lower index) are selected, and the last token
+ * is always selected when force_last != 0.  mask u8 [B, tokens] out; positions
+ * (optional) i32 [B, tokens] ascending selected positions; counts (optional) i32 [B].
+ * Returns FL_E_INVALID if the forced last token is ineligible (checked on device:
+ * *error_flag set to 1 and the row left empty).
+ */
+int32_t fl_hidden_delta_score(const uint16_t* cur, const uint16_t* prev, int64_t rows,
+                              int32_t dim, float* score, void* stream);
+int32_t fl_select_tokens(const float* scores, int32_t batch, int32_t tokens, double fraction,
+                         const uint8_t* eligible, int32_t force_last, uint8_t* mask,
+                         int32_t* positions, int32_t* counts, int32_t* error_flag,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHLOOP_AMD_H */

@@ -1,0 +1,53 @@
+"""The C-ABI library loads and exports every symbol include/flashloop_amd.h declares
+(CPU only: no compute call is made; only argument validation that fails before any
+HIP call is exercised)."""
+
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from flashloop_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_functions():
+    text = (ROOT / "include" / "flashloop_amd.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_signatures():
+    assert _declared_functions() == sorted(_lib.SIGNATURES)
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(str(_lib.LIB_PATH))
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
+def test_argument_errors_are_reported_without_launching():
+    lib = _lib.load()
+    assert lib.fl_abi_version() == 1
+    rc = lib.fl_decode_topk(None, 1, 1, None, 1, 0.1, 64, None, None, None, None, None, None)
+    assert rc == _lib.FL_E_INVALID
+    assert b"null" in lib.fl_last_error()
+    rc = lib.fl_decode_attn_dense(None, 0, None, None, None, 1.0, None, None, 0, None, 0, None)
+    assert rc == _lib.FL_E_INVALID and b"view" in lib.fl_last_error()
+    v = _lib.FlCacheView()
+    rc = lib.fl_decode_attn_dense(C.byref(v), 7, None, None, None, 1.0, None, None, 0, None, 0, None)
+    assert rc == _lib.FL_E_INVALID and b"loop" in lib.fl_last_error()
+    rc = lib.fl_select_tokens(None, 1, 4, 0.5, None, 1, None, None, None, None, None)
+    assert rc == _lib.FL_E_INVALID
+    rc = lib.fl_gather_rows(None, 0, 0, 0, None, 0, 0, 0, 0, None, 0, None, None)
+    assert rc == _lib.FL_E_INVALID
+
+
+def test_struct_layout_matches_header():
+    # 4 ints + int[4] + 26 pointers (8 B) + 2 pointers + 2 ints
+    assert C.sizeof(_lib.FlCacheView) == 4 * 4 + 4 * 4 + 26 * 8 + 2 * 8 + 2 * 4

@@ -1,0 +1,339 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle.
+
+Bars: codes, scales/zeros and selected indices bit-exact;
+attention outputs within 2e-2 max-abs and 1e-3 mean-abs.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import codec
+from oracle import tokens as OT
+
+from flashloop_amd import CrossLoopKVLayer, decode_attention_step, kernels
+from flashloop_amd.synthetic import SCALING, decode_workload, ragged_lengths
+
+from gpu_util import (
+    assert_close,
+    assert_layer_matches_chain,
+    flat_rows,
+    materialized,
+    np32,
+    oracle_prefix,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _masks(batch, tokens, seed, p3=0.3, p4=0.5):
+    rng = np.random.default_rng(seed)
+    m3 = rng.random((batch, tokens)) < p3
+    m4 = m3 & (rng.random((batch, tokens)) < p4)
+    m3[:, -1] = m4[:, -1] = True
+    return m3, m4
+
+
+def _build(w, m3=None, m4=None, recon=False, token_capacity=None):
+    ks = [w.cache(r)[0].to(DEV) for r in range(4)]
+    vs = [w.cache(r)[1].to(DEV) for r in range(4)]
+    kw = {}
+    if m3 is not None:
+        kw = dict(mask_loop3=torch.from_numpy(m3).to(DEV), mask_loop4=torch.from_numpy(m4).to(DEV))
+    layer = CrossLoopKVLayer.from_prefill(ks, vs, lengths=w.lengths, recon=recon, token_capacity=token_capacity, **kw)
+    torch.cuda.synchronize()
+    return layer
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_pack_bit_exact(masked):
+    print("case: pack B2 H3 T390 masked=%s" % masked, flush=True)
+    w = decode_workload(2, 3, 390, seed=11)
+    m3 = m4 = None
+    if masked:
+        m3, m4 = _masks(2, 390, 5)
+    layer = _build(w, m3, m4, recon=True)
+    nk, nv, chain, tp = oracle_prefix([w.cache(r)[0] for r in range(4)], [w.cache(r)[1] for r in range(4)], m3, m4)
+    assert tp == layer.quantized_tokens == 320
+    assert_layer_matches_chain(layer, chain, tp, 2, 3)
+    for r in range(4):
+        got_k = np32(layer.recon_keys[r]).reshape(2, 3, 390, 128)[:, :, :tp]
+        got_v = np32(layer.recon_values[r]).reshape(2, 3, 390, 128)[:, :, :tp]
+        assert np.array_equal(got_k, chain.recon_keys[r]), f"R_{r} keys differ"
+        assert np.array_equal(got_v, chain.recon_values[r]), f"R_{r} values differ"
+
+
+def test_pack_closed_forms():
+    """Constant and ramp groups through the GPU codec (known answers)."""
+    print("case: pack closed forms", flush=True)
+    t = 128
+    k = torch.full((1, 1, t + 64, 128), 0.75, dtype=torch.bfloat16)
+    ramp = (-1.0 + 0.125 * (torch.arange(t + 64) % 16)).to(torch.bfloat16)
+    v = ramp[None, None, :, None].expand(1, 1, t + 64, 128).contiguous()
+    layer = CrossLoopKVLayer.from_prefill([k.to(DEV)] * 4, [v.to(DEV)] * 4)
+    kc = layer.key_codes[0].cpu().numpy()[0, :t]
+    km = layer.key_meta[0].cpu().numpy()[0, : t // 64]
+    assert np.all(kc == 0) and np.all(km[..., 0] == 1.0) and np.all(km[..., 1] == 0.75)
+    # loops 2-4 reproduce loop 1 exactly: zero residual codes with scale 1
+    for s in (1, 2, 3):
+        assert np.all(layer.key_codes[s].cpu().numpy()[0, :t] == 0)
+        assert np.all(layer.key_meta[s].cpu().numpy()[0, : t // 64, :, 0] == 1.0)
+
+
+def _oracle_rows(w, m3=None, m4=None):
+    """Per-(b,h) K_r/V_r rows ``[T_b, 128]`` for every loop, each sequence encoded on its own."""
+    K = [[] for _ in range(4)]
+    V = [[] for _ in range(4)]
+    h = w.keys[0].shape[1]
+    for b, t in enumerate(w.lengths):
+        ks = [w.keys[r][b : b + 1, :, :t] for r in range(4)]
+        vs = [w.values[r][b : b + 1, :, :t] for r in range(4)]
+        mm3 = None if m3 is None else m3[b : b + 1, :t]
+        mm4 = None if m4 is None else m4[b : b + 1, :t]
+        nk, nv, chain, tp = oracle_prefix(ks, vs, mm3, mm4)
+        Kb, Vb = materialized(nk, nv, chain, tp)
+        for r in range(4):
+            for j in range(h):
+                K[r].append(Kb[r][0, j])
+                V[r].append(Vb[r][0, j])
+    return K, V
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_dense_reader_all_loops(masked):
+    print("case: dense reader B2 H3 T390 masked=%s" % masked, flush=True)
+    w = decode_workload(2, 3, 390, seed=12)
+    m3 = m4 = None
+    if masked:
+        m3, m4 = _masks(2, 390, 6)
+    layer = _build(w, m3, m4)
+    K, V = _oracle_rows(w, m3, m4)
+    for loop in range(4):
+        kc, vc = w.current(loop)
+        out, logits = layer.dense_source_attention(
+            loop, query=w.queries[loop].to(DEV), current_key=kc.to(DEV), current_value=vc.to(DEV),
+            scaling=SCALING, return_logits=True)
+        torch.cuda.synchronize()
+        q = np32(w.queries[loop]).reshape(6, 128)
+        want, want_lg = OA.dense_decode(q, K[loop], V[loop], np32(kc).reshape(6, 128),
+                                        np32(vc).reshape(6, 128), SCALING)
+        assert_close(np32(out).reshape(6, 128), want, what=f"loop {loop} output")
+        assert_close(np32(logits).reshape(6, -1), want_lg, max_abs=2e-2, mean_abs=5e-3, what=f"loop {loop} logits")
+
+
+def test_topk_bit_exact_with_ties():
+    print("case: topk ties", flush=True)
+    rng = np.random.default_rng(3)
+    rows, n = 5, 3000
+    lg = rng.integers(-40, 40, size=(rows, n)).astype(np.float32) / 8.0  # many exact ties
+    lg[4] = 0.0  # all equal
+    for frac in (0.1, 0.37, 1.0):
+        sel = OA.decode_topk(lg, frac)
+        cap = sel.indices.shape[1]
+        t = torch.from_numpy(lg).to(DEV)
+        nk = torch.full((rows,), n, dtype=torch.int32, device=DEV)
+        idx, valid, mass, wts, counts = kernels.decode_topk(t, nk, frac, cap)
+        torch.cuda.synchronize()
+        assert np.array_equal(idx.cpu().numpy(), sel.indices), f"indices differ at fraction {frac}"
+        assert np.array_equal(valid.cpu().numpy().astype(bool), sel.valid)
+        assert np.array_equal(counts.cpu().numpy(), sel.count)
+        assert np.allclose(mass.cpu().numpy(), sel.mass, rtol=2e-6, atol=1e-7)
+        assert np.allclose(wts.cpu().numpy(), sel.selected_weights, rtol=2e-5, atol=1e-8)
+
+
+def test_topk_ragged_rows_and_budget_edges():
+    print("case: topk ragged", flush=True)
+    rng = np.random.default_rng(4)
+    n_keys = [1, 7, 64, 640, 641, 5000]
+    rows = len(n_keys)
+    lg = rng.standard_normal((rows, 5000)).astype(np.float32) * 3
+    frac = 0.1
+    cap = max(OA.padded_capacity(OA.decode_budget(n, frac)) for n in n_keys)
+    t = torch.from_numpy(lg).to(DEV)
+    idx, valid, mass, wts, counts = kernels.decode_topk(t, torch.tensor(n_keys, dtype=torch.int32, device=DEV), frac, cap)
+    torch.cuda.synchronize()
+    sel = OA.decode_topk([lg[r, :n] for r, n in enumerate(n_keys)], frac, kpad=cap)
+    assert np.array_equal(idx.cpu().numpy(), sel.indices)
+    assert np.array_equal(valid.cpu().numpy().astype(bool), sel.valid)
+    assert np.allclose(mass.cpu().numpy(), sel.mass, rtol=2e-6)
+
+
+def _step_vs_oracle(w, layer, m3=None, m4=None, frac=0.10):
+    b, h = len(w.lengths), w.keys[0].shape[1]
+    R = b * h
+    Kr, Vr = _oracle_rows(w, m3, m4)
+    qs = [w.queries[r].to(DEV) for r in range(4)]
+    cur = [w.current(r) for r in range(4)]
+    ks = [c[0].to(DEV) for c in cur]
+    vs = [c[1].to(DEV) for c in cur]
+    step = decode_attention_step(layer, qs, ks, vs, SCALING, frac)
+    torch.cuda.synchronize()
+    lengths = [x for x in w.lengths for _ in range(h)]
+    q = [np32(w.queries[r]).reshape(R, 128) for r in range(4)]
+    kc = [np32(c[0]).reshape(R, 128) for c in cur]
+    vc = [np32(c[1]).reshape(R, 128) for c in cur]
+    o0, _ = OA.dense_decode(q[0], Kr[0], Vr[0], kc[0], vc[0], SCALING)
+    o1, lg1 = OA.dense_decode(q[1], Kr[1], Vr[1], kc[1], vc[1], SCALING)
+    assert_close(np32(step.out0).reshape(R, 128), o0, what="loop-1 output")
+    assert_close(np32(step.out1).reshape(R, 128), o1, what="loop-2 output")
+    # selection: bit-exact on the kernel's own logits (identical inputs)
+    g_lg = np32(step.logits1).reshape(R, -1)
+    rows_lg = [g_lg[r, : lengths[r] + 1] for r in range(R)]
+    cap = step.indices.shape[-1]
+    sel = OA.decode_topk(rows_lg, frac, kpad=cap)
+    assert np.array_equal(step.indices.cpu().numpy().reshape(R, cap), sel.indices), "selected indices differ"
+    # end-to-end selection overlap against the oracle's own logits (reported, not bit-exact)
+    sel_o = OA.decode_topk(lg1, frac, kpad=cap)
+    overlap = np.mean([
+        len(set(sel.indices[r, : sel.count[r]]) & set(sel_o.indices[r, : sel_o.count[r]])) / sel_o.count[r]
+        for r in range(R)
+    ])
+    assert overlap > 0.97, f"selection overlap with oracle logits {overlap:.4f}"
+    # selected aggregate and cached-mass deltas, oracle run on the kernel's selection
+    so = OA.selected_value_aggregate(sel.indices, sel.valid, sel.selected_weights, Vr[1], vc[1], lengths)
+    assert_close(np32(step.selected_output).reshape(R, 128), so, what="selected output")
+    for loop, got in ((2, step.delta2), (3, step.delta3)):
+        want = OA.sparse_delta(q[loop], Kr[loop], Vr[loop], kc[loop], vc[loop], lengths, sel.indices, sel.valid,
+                               so, sel.mass, SCALING)
+        assert_close(np32(got).reshape(R, 128), want, what=f"loop-{loop + 1} delta")
+    return overlap
+
+
+def test_decode_step_uniform():
+    print("case: decode step B2 H4 T1200", flush=True)
+    w = decode_workload(2, 4, 1200, seed=3)
+    layer = _build(w)
+    _step_vs_oracle(w, layer)
+
+
+def test_decode_step_masked_late_loops():
+    print("case: decode step masked B1 H4 T900", flush=True)
+    w = decode_workload(1, 4, 900, seed=4)
+    m3, m4 = _masks(1, 900, 8, p3=0.25, p4=0.4)
+    layer = _build(w, m3, m4)
+    _step_vs_oracle(w, layer, m3, m4)
+
+
+def test_decode_step_ragged_batch():
+    print("case: decode step ragged B3 H2", flush=True)
+    lengths = ragged_lengths(3, 100, 900, seed=2)
+    lengths[0] = 100  # packed prefix of one group
+    w = decode_workload(3, 2, 0, seed=2, lengths=lengths)
+    layer = _build(w)
+    _step_vs_oracle(w, layer)
+
+
+def test_decode_step_full_fraction_equals_dense():
+    """fraction 1 selects every key: loop-2 output + delta == dense loop-3/4 output."""
+    print("case: full fraction", flush=True)
+    w = decode_workload(1, 2, 300, seed=9)
+    layer = _build(w)
+    qs = [w.queries[r].to(DEV) for r in range(4)]
+    cur = [w.current(r) for r in range(4)]
+    step = decode_attention_step(layer, qs, [c[0].to(DEV) for c in cur], [c[1].to(DEV) for c in cur], SCALING, 1.0)
+    for loop, d in ((2, step.delta2), (3, step.delta3)):
+        dense, _ = layer.dense_source_attention(loop, query=qs[loop], current_key=cur[loop][0].to(DEV),
+                                                current_value=cur[loop][1].to(DEV), scaling=SCALING,
+                                                return_logits=False)
+        got = np32(step.out1 + d)
+        assert np.abs(got - np32(dense)).max() < 2e-4
+
+
+def test_decode_append_and_rollover_bit_exact():
+    """Appending decode tokens rolls groups out of the tail (cfg1 semantics): the packed
+    streams must equal the oracle's encoding of the whole sequence."""
+    print("case: append/rollover", flush=True)
+    t0, steps = 190, 75
+    w = decode_workload(1, 2, t0, seed=1, extra=steps + 1)
+    m3, m4 = _masks(1, t0, 9)
+    ks = [w.keys[r][:, :, :t0].contiguous().to(DEV) for r in range(4)]
+    vs = [w.values[r][:, :, :t0].contiguous().to(DEV) for r in range(4)]
+    layer = CrossLoopKVLayer.from_prefill(ks, vs, mask_loop3=torch.from_numpy(m3).to(DEV),
+                                          mask_loop4=torch.from_numpy(m4).to(DEV), token_capacity=512)
+    for i in range(steps):
+        p = t0 + i
+        layer.append_decode_token([w.keys[r][:, :, p:p + 1].to(DEV) for r in range(4)],
+                                  [w.values[r][:, :, p:p + 1].to(DEV) for r in range(4)])
+    torch.cuda.synchronize()
+    total = t0 + steps
+    assert layer.quantized_tokens == codec.packed_prefix_tokens(total)
+    nk = [np32(w.keys[r][:, :, :total]) for r in range(4)]
+    nv = [np32(w.values[r][:, :, :total]) for r in range(4)]
+    chain, tp = codec.compress_prefix(nk, nv, (m3, m4))
+    assert_layer_matches_chain(layer, chain, tp, 1, 2)
+    # and the reader over the rolled cache matches the oracle
+    (K, V) = materialized(nk, nv, chain, tp)
+    kc, vc = w.keys[1][:, :, total:total + 1], w.values[1][:, :, total:total + 1]
+    out, _ = layer.dense_source_attention(1, query=w.queries[1].to(DEV), current_key=kc.to(DEV),
+                                          current_value=vc.to(DEV), scaling=SCALING, return_logits=False)
+    want, _ = OA.dense_decode(np32(w.queries[1]).reshape(2, 128), flat_rows(K[1]), flat_rows(V[1]),
+                              np32(kc).reshape(2, 128), np32(vc).reshape(2, 128), SCALING)
+    assert_close(np32(out).reshape(2, 128), want, what="post-rollover output")
+
+
+def test_rows_gather_scatter_round_trip():
+    print("case: rows", flush=True)
+    g = torch.Generator().manual_seed(0)
+    hidden = torch.randn(1, 1000, 2048, generator=g).to(torch.bfloat16)
+    kv = torch.randn(1, 16, 1000, 128, generator=g).to(torch.bfloat16)
+    pos = torch.sort(torch.randperm(1000, generator=g)[:250]).values.to(torch.int32)
+    hd, kvd, pd = hidden.to(DEV), kv.to(DEV), pos.to(DEV)
+    gh, err = kernels.gather_rows(hd, pd, 1)
+    gk, err2 = kernels.gather_rows(kvd, pd, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(gh.cpu(), hidden.index_select(1, pos.long()))
+    assert torch.equal(gk.cpu(), kv.index_select(2, pos.long()))
+    assert int(err.item()) == 0 and int(err2.item()) == 0
+    new = torch.randn_like(gk.cpu())
+    dst = kvd.clone()
+    kernels.scatter_rows_(dst, pd, new.to(DEV), 2)
+    want = kv.clone().index_copy_(2, pos.long(), new)
+    assert torch.equal(dst.cpu(), want)
+    assert np.array_equal(dst.cpu().float().numpy(), OT.scatter_rows(np32(kv), pos.numpy(), np32(new), 2))
+    # odd row size (4-byte path) and an out-of-range index is reported, not read
+    small = torch.arange(2 * 10 * 6, dtype=torch.int16, device=DEV).reshape(2, 10, 6)
+    bad = torch.tensor([0, 9, 10], dtype=torch.int32, device=DEV)
+    got, err = kernels.gather_rows(small, bad, 1)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    assert torch.equal(got[:, :2].cpu(), small.cpu()[:, [0, 9]])
+
+
+def test_hidden_score_and_token_selection():
+    print("case: token selection", flush=True)
+    g = torch.Generator().manual_seed(1)
+    h1 = torch.randn(2, 777, 2048, generator=g).to(torch.bfloat16)
+    h2 = (h1.float() + 0.3 * torch.randn(2, 777, 2048, generator=g)).to(torch.bfloat16)
+    s = kernels.hidden_delta_score(h2.to(DEV), h1.to(DEV))
+    torch.cuda.synchronize()
+    want = OT.hidden_delta_score(np32(h2), np32(h1))
+    assert np.allclose(s.cpu().numpy(), want, rtol=1e-5)
+    sc = s.cpu().numpy()
+    mask3, pos3, cnt3, err = kernels.select_tokens(s, 0.25)
+    torch.cuda.synchronize()
+    want3 = OT.select_active_mask(sc, 0.25)
+    assert np.array_equal(mask3.cpu().numpy(), want3)
+    assert int(err.item()) == 0
+    mask4, pos4, cnt4, err = kernels.select_tokens(s * 0.5, 0.10, eligible=mask3)
+    torch.cuda.synchronize()
+    want4 = OT.select_active_mask(sc * 0.5, 0.10, eligible=want3)
+    assert np.array_equal(mask4.cpu().numpy(), want4)
+    assert np.all(~want4 | want3)
+    for b in range(2):
+        n = int(cnt4[b].item())
+        assert n == math.ceil(777 * 0.10)
+        assert np.array_equal(pos4[b, :n].cpu().numpy(), np.nonzero(want4[b])[0])
+    # ties: equal scores pick lower indices; an ineligible forced token is an error
+    flat = torch.zeros(1, 50, device=DEV)
+    m, p, c, err = kernels.select_tokens(flat, 0.1)
+    torch.cuda.synchronize()
+    assert np.array_equal(np.nonzero(m.cpu().numpy()[0])[0], [0, 1, 2, 3, 49])
+    el = torch.ones(1, 50, dtype=torch.bool, device=DEV)
+    el[0, 49] = False
+    m, p, c, err = kernels.select_tokens(flat, 0.1, eligible=el)
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
