@@ -225,7 +225,8 @@ class CrossLoopKVLayer:
 
     # ------------------------------------------------------------------ readers
     def logits_capacity(self) -> int:
-        return self.token_count + 1
+        """Row stride of the logits buffer: covers the longest prefix plus the longest tail."""
+        return self.quantized_tokens + self.tail_tokens_max + 1
 
     def dense_source_attention(self, loop: int, *, query, current_key, current_value, scaling: float,
                                return_logits: bool):
