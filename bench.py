@@ -3,7 +3,8 @@
 A step is one layer's decode attention over all four loops of the cfg3 workload
 (B=8, H=16, D=128, T=32768; int4 residual streams g64, BF16 tail 64; loops 3-4 attend to
 the top 10% of keys ranked by the loop-2 logits): dense loop 1, dense loop 2 with
-logits, top-k selection, loop-2 selected aggregate, cached-mass sparse loops 3 and 4
+logits, top-k selection, cached-mass sparse loop 3 (which also forms the loop-2
+selected aggregate from the rows it reads) and sparse loop 4
 (flashloop/engine.py:422-531).  The packed cache is built once on the GPU before timing
 (inputs resident in HBM).  Prints one JSON line.
 
@@ -41,6 +42,9 @@ def parse():
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=8, help="(b,h) rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--fraction", type=float, default=0.10)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="run one device copy of this many MiB first (a known-size kernel that "
+                         "calibrates rocprof FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -107,6 +111,12 @@ def main():
     torch.cuda.empty_cache()
     kcur = [c[0] for c in cur]
     vcur = [c[1] for c in cur]
+    if args.calib_copy_mib > 0:
+        src = torch.ones(args.calib_copy_mib * 2**18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     def step():
         return decode_attention_step(layer, queries, kcur, vcur, SCALING, args.fraction)
@@ -123,10 +133,9 @@ def main():
                                                     scaling=SCALING, return_logits=True)
         ev[i][1].record(stream)
         idx, valid, mass, wts, counts = layer.select_decode_keys(logits, args.fraction)
-        so = layer.pv(1, wts, idx, valid, vcur[1])
-        d2 = layer.cached_mass_sparse_attention_delta(2, query=queries[2], current_key=kcur[2], current_value=vcur[2],
-                                                      indices=idx, valid=valid, source_selected_output=so,
-                                                      global_mass=mass, scaling=SCALING)
+        d2, so = layer.cached_mass_sparse_attention_delta_with_source(
+            2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
+            source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)
         d3 = layer.cached_mass_sparse_attention_delta(3, query=queries[3], current_key=kcur[3], current_value=vcur[3],
                                                       indices=idx, valid=valid, source_selected_output=so,
                                                       global_mass=mass, scaling=SCALING)
@@ -155,8 +164,7 @@ def main():
         "dense_loop1": accounting.dense_bytes(packed, tail, 1, False),
         "dense_loop2": accounting.dense_bytes(packed, tail, 2, True),
         "topk": accounting.topk_bytes(packed, tail, cap),
-        "selected_pv": accounting.selected_pv_bytes(stats, cap),
-        "sparse_loop3": accounting.sparse_bytes(stats, cap, 2),
+        "sparse_loop3_with_source": accounting.sparse_bytes(stats, cap, 2, with_source=True),
         "sparse_loop4": accounting.sparse_bytes(stats, cap, 3),
     }
     step_bytes = sum(parts.values())

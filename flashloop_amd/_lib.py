@@ -12,7 +12,7 @@ import ctypes as C
 import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libflashloop_amd.so"
+LIB_PATH = Path(os.environ.get("FLASHLOOP_AMD_LIB", Path(__file__).resolve().parent / "libflashloop_amd.so"))
 
 FL_OK = 0
 FL_E_INVALID = -1
@@ -68,6 +68,10 @@ SIGNATURES = {
     "fl_decode_attn_sparse_delta": (
         _I32,
         [_VIEW, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _F32, _P, _P, _SZ, _P],
+    ),
+    "fl_decode_attn_sparse_delta_fused": (
+        _I32,
+        [_VIEW, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _F32, _P, _P, _P, _SZ, _P],
     ),
     "fl_gather_rows": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "fl_scatter_rows": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),

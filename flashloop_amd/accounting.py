@@ -66,10 +66,15 @@ def selected_pv_bytes(stats, cap: int, streams: int = 2) -> int:
     return tot
 
 
-def sparse_bytes(stats, cap: int, loop: int) -> int:
-    """Cached-mass sparse reader of loop index ``loop`` (2 or 3): streams 0..loop."""
+def sparse_bytes(stats, cap: int, loop: int, with_source: bool = False) -> int:
+    """Cached-mass sparse reader of loop index ``loop`` (2 or 3): streams 0..loop.
+    ``with_source``: the pass also forms the loop-2 selected aggregate -- its V rows of
+    streams 0/1 are already counted; add the weights, loop-2 tail/current V rows and
+    the aggregate written."""
     tot = 0
     for s in stats:
+        if with_source:
+            tot += cap * 4 + s["other"] * BF16_ROW + 128 * 4
         rows_per_stream = [s["prefix"], s["prefix"], s["s2"], s["s3"]][: loop + 1]
         for n in rows_per_stream:
             tot += n * (2 * CODE_ROW + VMETA_ROW)

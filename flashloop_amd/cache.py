@@ -275,6 +275,21 @@ class CrossLoopKVLayer:
         )
         return out.view(self.batch, self.heads, 1, HEAD_DIM)
 
+    def cached_mass_sparse_attention_delta_with_source(self, loop: int, *, query, current_key, current_value,
+                                                       indices, valid, source_weights, source_current_value,
+                                                       global_mass, scaling: float):
+        """Loop-3 form of ``cached_mass_sparse_attention_delta`` that also returns the loop-2
+        selected aggregate (``_selected_value_aggregate``, flashloop/engine.py:346-371) from
+        the same pass over the selected rows.  Returns ``(delta, source_output)``."""
+        if int(loop) not in (2, 3):
+            raise ValueError("cached-mass sparse attention is only valid for Loop 3/4")
+        out, src = kernels.fused_sparse_attention_delta_with_source(
+            self.view(), int(loop), query, current_key, current_value, indices, valid, source_weights,
+            source_current_value, global_mass, scaling, device=self.device, workspace=self.workspace,
+        )
+        shape = (self.batch, self.heads, 1, HEAD_DIM)
+        return out.view(shape), src.view(shape)
+
     # ------------------------------------------------------------------ decode append
     def append_decode_token(self, keys: Sequence[torch.Tensor], values: Sequence[torch.Tensor]) -> None:
         """``append_decode_token`` (flashloop/cache.py:1758-1776): write the step's four loop
@@ -427,20 +442,29 @@ class AttentionStep:
 
 
 def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scaling: float,
-                          fraction: float = 0.10) -> AttentionStep:
+                          fraction: float = 0.10, fused_source: bool = True) -> AttentionStep:
     """One layer's decode attention over four loops (flashloop/engine.py:422-531, before
     ``o_proj``): dense loops 1-2 (loop 2 with logits), loop-2 key selection and selected
     aggregate, then the cached-mass deltas of loops 3-4.  ``queries/keys/values``: four
-    bf16 ``[B,H,1,128]`` (the current token of each loop)."""
+    bf16 ``[B,H,1,128]`` (the current token of each loop).
+
+    With ``fused_source`` the loop-2 selected aggregate is formed by the loop-3 reader
+    from the rows it reads anyway (it is first consumed there, engine.py:511-528);
+    otherwise it is a separate selected-PV pass at loop 2, as in the reference."""
     out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=keys[0], current_value=values[0],
                                            scaling=scaling, return_logits=False)
     out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=keys[1], current_value=values[1],
                                                 scaling=scaling, return_logits=True)
     idx, valid, mass, w, counts = layer.select_decode_keys(logits, fraction)
-    so = layer.pv(1, w, idx, valid, values[1])
-    d2 = layer.cached_mass_sparse_attention_delta(2, query=queries[2], current_key=keys[2], current_value=values[2],
-                                                  indices=idx, valid=valid, source_selected_output=so,
-                                                  global_mass=mass, scaling=scaling)
+    if fused_source:
+        d2, so = layer.cached_mass_sparse_attention_delta_with_source(
+            2, query=queries[2], current_key=keys[2], current_value=values[2], indices=idx, valid=valid,
+            source_weights=w, source_current_value=values[1], global_mass=mass, scaling=scaling)
+    else:
+        so = layer.pv(1, w, idx, valid, values[1])
+        d2 = layer.cached_mass_sparse_attention_delta(2, query=queries[2], current_key=keys[2],
+                                                      current_value=values[2], indices=idx, valid=valid,
+                                                      source_selected_output=so, global_mass=mass, scaling=scaling)
     d3 = layer.cached_mass_sparse_attention_delta(3, query=queries[3], current_key=keys[3], current_value=values[3],
                                                   indices=idx, valid=valid, source_selected_output=so,
                                                   global_mass=mass, scaling=scaling)

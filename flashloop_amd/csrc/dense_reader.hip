@@ -34,9 +34,117 @@ struct DenseArgs {
   float* logits;
   int64_t logits_stride;
   float* ws;  // [B*H, nsplit+1, kPartial]
+  float* out;
   int nsplit;
   int gps;    // groups per prefix split
 };
+
+// Registers of one half-group (32 tokens, 2 per lane): K/V codes and V metadata of
+// every stream, plus (first half only) the group's K metadata for this lane's 2 channels.
+template <int NS>
+struct HalfSet {
+  float4 kmeta[NS];
+  uint4 kw[2][NS];
+  uint4 vw[2][NS];
+  float2 vm[2][NS];
+  bool has[2][NS];
+};
+
+template <int NS>
+__device__ __forceinline__ void load_half(HalfSet<NS>& hs, const fl_cache_view& v, int bh, int b, int gi, int h,
+                                          int row, int quarter, int gcap) {
+  const int lane = threadIdx.x & 63;
+  if (h == 0) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      hs.kmeta[s] = *reinterpret_cast<const float4*>(
+          v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + gi) * kDim + 2 * lane) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int t = gi * kGroup + row + 16 * (2 * h + i);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      int r = t;
+      if (s >= 2) r = v.rank[s - 2][static_cast<int64_t>(b) * v.token_capacity + t];
+      hs.has[i][s] = r >= 0 && r < v.row_capacity[s];
+      if (!hs.has[i][s]) r = 0;
+      const int64_t rowi = static_cast<int64_t>(bh) * v.row_capacity[s] + r;
+      hs.kw[i][s] = *reinterpret_cast<const uint4*>(v.key_codes[s] + rowi * kRowBytes + 16 * quarter);
+      hs.vw[i][s] = *reinterpret_cast<const uint4*>(v.value_codes[s] + rowi * kRowBytes + 16 * quarter);
+      hs.vm[i][s] = *reinterpret_cast<const float2*>(v.value_meta[s] + (rowi * 2 + (quarter >> 1)) * 2);
+    }
+  }
+}
+
+// Logits, online softmax and P.V for one half-group.  At h == 0 the group's q*scale
+// products (LDS, wave-private) and q.min constants are rebuilt from hs.kmeta.
+template <int NS>
+__device__ __forceinline__ void dense_half(HalfSet<NS>& hs, QuadState& st, const DenseArgs& a, const float* qf,
+                                           float (*qsh)[kDim], int b, int gi, int h, int row, int quarter,
+                                           float* lrow) {
+  const int lane = threadIdx.x & 63;
+  __shared__ float cs_sh[kWaves][4];
+  float* cs = cs_sh[threadIdx.x >> 6];
+  if (h == 0) {
+    const float q0 = qf[2 * lane], q1 = qf[2 * lane + 1];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      qsh[s][2 * lane] = q0 * hs.kmeta[s].x;
+      qsh[s][2 * lane + 1] = q1 * hs.kmeta[s].z * 0.0625f;  // odd channel: high nibble reads 16*code
+      const float c = wave_sum(fmaf(q0, hs.kmeta[s].y, q1 * hs.kmeta[s].w));
+      if (lane == 0) cs[s] = c;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  float lg[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    float qe[16], qo[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 x = *reinterpret_cast<const float4*>(&qsh[s][32 * quarter + 8 * k]);
+      const float4 y = *reinterpret_cast<const float4*>(&qsh[s][32 * quarter + 8 * k + 4]);
+      qe[4 * k + 0] = x.x; qo[4 * k + 0] = x.y;
+      qe[4 * k + 1] = x.z; qo[4 * k + 1] = x.w;
+      qe[4 * k + 2] = y.x; qo[4 * k + 2] = y.y;
+      qe[4 * k + 3] = y.z; qo[4 * k + 3] = y.w;
+    }
+    const float c = cs[s];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float d = 0.0f;
+      d = dot8(hs.kw[i][s].x, qe + 0, qo + 0, d);
+      d = dot8(hs.kw[i][s].y, qe + 4, qo + 4, d);
+      d = dot8(hs.kw[i][s].z, qe + 8, qo + 8, d);
+      d = dot8(hs.kw[i][s].w, qe + 12, qo + 12, d);
+      d = quad_sum(d) + c;
+      if (s < 2 || hs.has[i][s]) lg[i] += d;
+    }
+  }
+  if (lrow && quarter == 0) {
+    lrow[gi * kGroup + row + 16 * (2 * h)] = lg[0];
+    lrow[gi * kGroup + row + 16 * (2 * h + 1)] = lg[1];
+  }
+  float p[2];
+  online_update(st, lg, p, 2);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      if (s >= 2 && !hs.has[i][s]) continue;
+      const float we = p[i] * hs.vm[i][s].x;
+      const float wo = we * 0.0625f;
+      st.mu = fmaf(p[i], hs.vm[i][s].y, st.mu);
+      axpy8(hs.vw[i][s].x, we, wo, st.acc + 0);
+      axpy8(hs.vw[i][s].y, we, wo, st.acc + 8);
+      axpy8(hs.vw[i][s].z, we, wo, st.acc + 16);
+      axpy8(hs.vw[i][s].w, we, wo, st.acc + 24);
+    }
+  }
+}
 
 template <int NS>
 __global__ __launch_bounds__(kThreads) void dense_reader_kernel(DenseArgs a) {
@@ -73,97 +181,23 @@ __global__ __launch_bounds__(kThreads) void dense_reader_kernel(DenseArgs a) {
     const int g_begin = split * a.gps;
     const int g_end = min(g_begin + a.gps, G);
     const int gcap = v.token_capacity / kGroup;
-    for (int gi = g_begin + wave; gi < g_end; gi += kWaves) {
-      // ---- per-group q*scale and q.min in LDS (wave-private region)
-      float cs[NS];
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const float4 meta = *reinterpret_cast<const float4*>(
-            v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + gi) * kDim + 2 * lane) * 2);
-        const float q0 = qf[2 * lane], q1 = qf[2 * lane + 1];
-        qsh[wave][s][2 * lane] = q0 * meta.x;
-        qsh[wave][s][2 * lane + 1] = q1 * meta.z * 0.0625f;  // odd channel: high nibble reads 16*code
-        cs[s] = wave_sum(fmaf(q0, meta.y, q1 * meta.w));
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-      // ---- load K and V codes of this lane's 4 tokens (all streams) up front
-      uint4 kw[4][NS], vw[4][NS];
-      float2 vm[4][NS];
-      bool has[4][NS];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = gi * kGroup + row + 16 * i;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          int r = t;
-          if (s >= 2) r = v.rank[s - 2][static_cast<int64_t>(b) * v.token_capacity + t];
-          has[i][s] = r >= 0 && r < v.row_capacity[s];
-          if (!has[i][s]) r = 0;
-          const int64_t rowi = static_cast<int64_t>(bh) * v.row_capacity[s] + r;
-          kw[i][s] = *reinterpret_cast<const uint4*>(v.key_codes[s] + rowi * kRowBytes + 16 * quarter);
-          vw[i][s] = *reinterpret_cast<const uint4*>(v.value_codes[s] + rowi * kRowBytes + 16 * quarter);
-          vm[i][s] = *reinterpret_cast<const float2*>(v.value_meta[s] + (rowi * 2 + (quarter >> 1)) * 2);
-        }
-      }
-
-      // ---- logits
-      float lg[4];
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        float qe[16], qo[16];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float4 x = *reinterpret_cast<const float4*>(&qsh[wave][s][32 * quarter + 8 * k]);
-          const float4 y = *reinterpret_cast<const float4*>(&qsh[wave][s][32 * quarter + 8 * k + 4]);
-          qe[4 * k + 0] = x.x; qo[4 * k + 0] = x.y;
-          qe[4 * k + 1] = x.z; qo[4 * k + 1] = x.w;
-          qe[4 * k + 2] = y.x; qo[4 * k + 2] = y.y;
-          qe[4 * k + 3] = y.z; qo[4 * k + 3] = y.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float d = 0.0f;
-          d = dot8(kw[i][s].x, qe + 0, qo + 0, d);
-          d = dot8(kw[i][s].y, qe + 4, qo + 4, d);
-          d = dot8(kw[i][s].z, qe + 8, qo + 8, d);
-          d = dot8(kw[i][s].w, qe + 12, qo + 12, d);
-          d += shfl_xor(d, 1);
-          d += shfl_xor(d, 2);
-          d += cs[s];
-          if (s == 0) lg[i] = d;
-          else if (s < 2 || has[i][s]) lg[i] += d;
-        }
-      }
-      if (lrow && quarter == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) lrow[gi * kGroup + row + 16 * i] = lg[i];
-      }
-
-      // ---- online softmax and P.V
-      float p[4];
-      online_update(st, lg, p, 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          if (s >= 2 && !has[i][s]) continue;
-          const float we = p[i] * vm[i][s].x;
-          const float wo = we * 0.0625f;
-          st.mu = fmaf(p[i], vm[i][s].y, st.mu);
-          axpy8(vw[i][s].x, we, wo, st.acc + 0);
-          axpy8(vw[i][s].y, we, wo, st.acc + 8);
-          axpy8(vw[i][s].z, we, wo, st.acc + 16);
-          axpy8(vw[i][s].w, we, wo, st.acc + 24);
-        }
-      }
+    // This wave's work: groups g_begin+wave, +kWaves, ... each as two half-groups of 32
+    // tokens (2 per lane).  Unit u = 2*k + h covers half h of the wave's k-th group.
+    const int my_groups = (g_end - g_begin - wave + kWaves - 1) / kWaves;
+    const int units = g_end - g_begin > wave ? 2 * my_groups : 0;
+    HalfSet<NS> set0, set1;
+    if (units > 0) load_half<NS>(set0, v, bh, b, g_begin + wave, 0, row, quarter, gcap);
+    for (int u = 0; u < units; u += 2) {
+      // ping-pong: the next unit's loads are in flight while this one computes
+      load_half<NS>(set1, v, bh, b, g_begin + wave + (u >> 1) * kWaves, 1, row, quarter, gcap);
+      dense_half<NS>(set0, st, a, qf, qsh[wave], b, g_begin + wave + (u >> 1) * kWaves, 0, row, quarter, lrow);
+      if (u + 2 < units) load_half<NS>(set0, v, bh, b, g_begin + wave + ((u >> 1) + 1) * kWaves, 0, row, quarter, gcap);
+      dense_half<NS>(set1, st, a, qf, qsh[wave], b, g_begin + wave + (u >> 1) * kWaves, 1, row, quarter, lrow);
     }
   } else {
     // ---- BF16 tail of this loop, then the current token (virtual row tl)
-    const uint16_t* tk = v.tail_key[a.loop] + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
-    const uint16_t* tv = v.tail_value[a.loop] + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
+    const uint16_t* tk = a.tail_k + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
+    const uint16_t* tv = a.tail_v + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
     const uint16_t* ck = a.kc + static_cast<int64_t>(bh) * kDim;
     const uint16_t* cv = a.vc + static_cast<int64_t>(bh) * kDim;
     float qr[32];
@@ -195,8 +229,7 @@ __global__ __launch_bounds__(kThreads) void dense_reader_kernel(DenseArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) vwords[k] = make_uint4(0, 0, 0, 0);
       }
-      d += shfl_xor(d, 1);
-      d += shfl_xor(d, 2);
+      d = quad_sum(d);
       float lg = valid ? d : -INFINITY;
       if (lrow && quarter == 0 && valid) lrow[Tp + vt] = lg;
       float p;
@@ -239,7 +272,8 @@ extern "C" size_t fl_decode_attn_dense_workspace(const fl_cache_view* view) {
   if (!view) return 0;
   const int gps = choose_gps(*view);
   const int ns = nsplit_of(*view, gps);
-  return static_cast<size_t>(view->batch) * view->heads * (ns + 1) * kPartial * sizeof(float);
+  const int rows = view->batch * view->heads;
+  return static_cast<size_t>(rows) * (ns + 1) * kPartial * sizeof(float);
 }
 
 extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop, const uint16_t* q,
@@ -267,6 +301,8 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   FL_REQUIRE(logits == nullptr || logits_stride >= static_cast<int64_t>(v.max_packed_tokens) + v.max_tail_tokens + 1,
              "fl_decode_attn_dense: logits_stride smaller than the key count");
   FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense: workspace too small");
+  FL_REQUIRE(nsplit_of(v, choose_gps(v)) + 1 <= kMergeMaxParts, "fl_decode_attn_dense: context too long for one merge");
+  FL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "fl_decode_attn_dense: workspace must be 16-byte aligned");
   DenseArgs a{};
   a.v = v;
   a.loop = loop;
@@ -279,6 +315,9 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   a.ws = static_cast<float*>(workspace);
   a.gps = choose_gps(v);
   a.nsplit = nsplit_of(v, a.gps);
+  a.out = out;
+  a.tail_k = v.tail_key[loop];
+  a.tail_v = v.tail_value[loop];
   const dim3 grid(a.nsplit + 1, v.batch * v.heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (loop) {
@@ -289,8 +328,9 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   }
   FL_LAUNCH_CHECK("fl_decode_attn_dense(reader)");
   hipLaunchKernelGGL(merge_partials_kernel, dim3(v.batch * v.heads), dim3(kDim), 0, st,
-                     static_cast<const float*>(a.ws), a.nsplit + 1, out, kMergeSoftmax,
-                     static_cast<const float*>(nullptr), static_cast<const float*>(nullptr));
+                     static_cast<const float*>(a.ws), a.nsplit + 1, out, static_cast<int>(kMergeSoftmax),
+                     static_cast<const float*>(nullptr), static_cast<const float*>(nullptr),
+                     static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
   FL_LAUNCH_CHECK("fl_decode_attn_dense(merge)");
   return FL_OK;
 }

@@ -57,20 +57,72 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
 
 // ---------------------------------------------------------------- wave reductions
+// Lane exchanges use DPP (a VALU operand modifier, no LDS round trip): quad_perm for
+// xor 1 / xor 2 inside a quad, row_half_mirror / row_mirror to fold 8 and 16 lanes, then
+// readlane for the four 16-lane rows of the wave.
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16
+
+// sum over the 4 lanes of a quad, result in every lane of the quad
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
   return v;
 }
+__device__ __forceinline__ float quad_min(float v) {
+  v = fminf(v, dpp<kDppXor1>(v));
+  return fminf(v, dpp<kDppXor2>(v));
+}
+__device__ __forceinline__ float quad_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  return fmaxf(v, dpp<kDppXor2>(v));
+}
+__device__ __forceinline__ int quad_sum_i(int v) {
+  v += dpp_i<kDppXor1>(v);
+  return v + dpp_i<kDppXor2>(v);
+}
+__device__ __forceinline__ float pair_min(float v) { return fminf(v, dpp<kDppXor1>(v)); }
+__device__ __forceinline__ float pair_max(float v) { return fmaxf(v, dpp<kDppXor1>(v)); }
+
+__device__ __forceinline__ float row_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// sum / max over the whole wave, result (uniform) in every lane
+__device__ __forceinline__ float wave_sum(float v) {
+  v = quad_sum(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
-  return v;
+  v = quad_max(v);
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
+}
+
+// Workgroup barrier that orders LDS only: global loads still in flight stay in flight
+// (__syncthreads also fences global memory, which drains every outstanding load).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // exp2 of a finite-or--inf argument (v_exp_f32); exp(x) = exp2(x*log2e)

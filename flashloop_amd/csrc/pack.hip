@@ -115,14 +115,11 @@ __global__ __launch_bounds__(256) void pack_groups_kernel(PackArgs a) {
           ++nact;
         }
       }
-#pragma unroll
-      for (int m = 1; m <= 2; m <<= 1) {
-        mn0 = fminf(mn0, shfl_xor(mn0, m));
-        mx0 = fmaxf(mx0, shfl_xor(mx0, m));
-        mn1 = fminf(mn1, shfl_xor(mn1, m));
-        mx1 = fmaxf(mx1, shfl_xor(mx1, m));
-        nact += shfl_xor(nact, m);
-      }
+      mn0 = quad_min(mn0);
+      mx0 = quad_max(mx0);
+      mn1 = quad_min(mn1);
+      mx1 = quad_max(mx1);
+      nact = quad_sum_i(nact);
       const Quant q0 = make_quant(mn0, mx0, nact > 0);
       const Quant q1 = make_quant(mn1, mx1, nact > 0);
       if (quarter == 0) {
@@ -201,8 +198,8 @@ __global__ __launch_bounds__(256) void pack_groups_kernel(PackArgs a) {
         mn = fminf(mn, x[c]);
         mx = fmaxf(mx, x[c]);
       }
-      mn = fminf(mn, shfl_xor(mn, 1));
-      mx = fmaxf(mx, shfl_xor(mx, 1));
+      mn = pair_min(mn);
+      mx = pair_max(mx);
       const Quant q = make_quant(mn, mx, act);
       uint32_t words[4] = {0, 0, 0, 0};
 #pragma unroll

@@ -12,17 +12,26 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kPartial = kDim + 2;  // m, l, acc[128]
 
 
+
+// Byte k of a register to float: these patterns select v_cvt_f32_ubyte{k} (one op).
 __device__ __forceinline__ float ubyte0(uint32_t w) { return static_cast<float>(w & 0xFFu); }
 __device__ __forceinline__ float ubyte1(uint32_t w) { return static_cast<float>((w >> 8) & 0xFFu); }
 __device__ __forceinline__ float ubyte2(uint32_t w) { return static_cast<float>((w >> 16) & 0xFFu); }
 __device__ __forceinline__ float ubyte3(uint32_t w) { return static_cast<float>(w >> 24); }
 
+// w & m through v_bitop3_b32 (truth table 0xC0 = S0 & S1).  A plain `&` lets the
+// combiner merge the nibble mask with the byte extraction into a bit-field extract,
+// which then costs a second instruction per code; bitop3 keeps one mask per word.
+__device__ __forceinline__ uint32_t nibble_mask(uint32_t w, uint32_t m) {
+  return __builtin_amdgcn_bitop3_b32(w, m, 0u, 0xC0);
+}
+
 // 8 nibbles of word w: bytes hold (even channel lo, odd channel hi).
 // acc += sum_e qe[e]*lo_e + qo[e]*hi_e, with qo pre-divided by 16 because the high
 // nibbles are converted in place (value 16*code).
 __device__ __forceinline__ float dot8(uint32_t w, const float* qe, const float* qo, float acc) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;
-  const uint32_t hi = w & 0xF0F0F0F0u;
+  const uint32_t lo = nibble_mask(w, 0x0F0F0F0Fu);
+  const uint32_t hi = nibble_mask(w, 0xF0F0F0F0u);
   acc = fmaf(qe[0], ubyte0(lo), acc);
   acc = fmaf(qe[1], ubyte1(lo), acc);
   acc = fmaf(qe[2], ubyte2(lo), acc);
@@ -36,8 +45,8 @@ __device__ __forceinline__ float dot8(uint32_t w, const float* qe, const float* 
 
 // acc[8 channels of word] += w_even*code (lo) and w_odd16*(16*code) (hi)
 __device__ __forceinline__ void axpy8(uint32_t w, float we, float wo, float* acc) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;
-  const uint32_t hi = w & 0xF0F0F0F0u;
+  const uint32_t lo = nibble_mask(w, 0x0F0F0F0Fu);
+  const uint32_t hi = nibble_mask(w, 0xF0F0F0F0u);
   acc[0] = fmaf(we, ubyte0(lo), acc[0]);
   acc[2] = fmaf(we, ubyte1(lo), acc[2]);
   acc[4] = fmaf(we, ubyte2(lo), acc[4]);
@@ -101,34 +110,66 @@ __device__ void write_partial(QuadState& st, float* part, float (*comb)[16][kDim
 
 enum MergeMode { kMergeSoftmax = 0, kMergeMassDelta = 1, kMergeSum = 2 };
 
-// Combine a row's split partials (m, l, acc[128]).
+// Combine a row's split partials (m, l, acc[128]); one workgroup of 128 threads per row.
 //   kMergeSoftmax:   out = sum_i e^{m_i-M} acc_i / sum_i e^{m_i-M} l_i
 //   kMergeMassDelta: out = mass * (softmax merge - src)
 //   kMergeSum:       out = sum_i acc_i
+//   kMergeMassDeltaFused: src = sum_i acc2_i (second partial set, written to src_out),
+//                    out = mass * (softmax merge - src)
+// The per-part weights e^{m_i-M} are formed once in LDS; the channel sums then issue
+// independent loads (unrolled) instead of a dependent chain per part.
+constexpr int kMergeMassDeltaFused = 3;
+constexpr int kMergeMaxParts = 4096;
+
 __global__ __launch_bounds__(kDim) void merge_partials_kernel(const float* ws, int nparts, float* out, int mode,
-                                                              const float* mass, const float* src) {
+                                                              const float* mass, const float* src,
+                                                              const float* ws2, float* src_out) {
+  __shared__ float f[kMergeMaxParts];
+  __shared__ float red[2];
   const int bh = blockIdx.x, c = threadIdx.x;
   const float* p = ws + static_cast<int64_t>(bh) * nparts * kPartial;
-  float res;
+  const int64_t o = static_cast<int64_t>(bh) * kDim + c;
+  const int n = min(nparts, kMergeMaxParts);
   if (mode == kMergeSum) {
     float acc = 0.0f;
-    for (int i = 0; i < nparts; ++i) acc += p[i * kPartial + 2 + c];
-    res = acc;
-  } else {
-    float M = -INFINITY;
-    for (int i = 0; i < nparts; ++i) M = fmaxf(M, p[i * kPartial]);
-    float L = 0.0f, acc = 0.0f;
-    for (int i = 0; i < nparts; ++i) {
-      const float m = p[i * kPartial];
-      if (m == -INFINITY) continue;
-      const float f = fast_exp2((m - M) * kLog2e);
-      L = fmaf(p[i * kPartial + 1], f, L);
-      acc = fmaf(p[i * kPartial + 2 + c], f, acc);
-    }
-    res = acc / L;
-    if (mode == kMergeMassDelta) res = mass[bh] * (res - src[static_cast<int64_t>(bh) * kDim + c]);
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) acc += p[i * kPartial + 2 + c];
+    out[o] = acc;
+    return;
   }
-  out[static_cast<int64_t>(bh) * kDim + c] = res;
+  float M = -INFINITY;
+  for (int i = c; i < n; i += kDim) M = fmaxf(M, p[i * kPartial]);
+  M = wave_max(M);
+  if ((c & 63) == 0) red[c >> 6] = M;
+  __syncthreads();
+  M = fmaxf(red[0], red[1]);
+  __syncthreads();
+  float L = 0.0f;
+  for (int i = c; i < n; i += kDim) {
+    const float m = p[i * kPartial];
+    const float fi = (m == -INFINITY) ? 0.0f : fast_exp2((m - M) * kLog2e);
+    f[i] = fi;
+    L = fmaf(p[i * kPartial + 1], fi, L);
+  }
+  L = wave_sum(L);
+  if ((c & 63) == 0) red[c >> 6] = L;
+  __syncthreads();
+  L = red[0] + red[1];
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int i = 0; i < n; ++i) acc = fmaf(p[i * kPartial + 2 + c], f[i], acc);
+  float res = acc / L;
+  if (mode == kMergeMassDelta) {
+    res = mass[bh] * (res - src[o]);
+  } else if (mode == kMergeMassDeltaFused) {
+    const float* p2 = ws2 + static_cast<int64_t>(bh) * nparts * kPartial;
+    float s = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) s += p2[i * kPartial + 2 + c];
+    src_out[o] = s;
+    res = mass[bh] * (res - s);
+  }
+  out[o] = res;
 }
 
 }  // namespace

@@ -25,6 +25,9 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
 
 struct TopkShared {
   uint32_t hist[256];
@@ -227,6 +230,255 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
   }
 }
 
+// LDS-resident variant for rows of at most kLdsKeys keys (gfx950: 160 KiB of LDS per
+// workgroup): the row is read from HBM once into LDS as order-preserving keys; the
+// radix passes and the compaction read LDS.  Histograms are split four ways to spread
+// LDS atomics.  The selected mass is sum_{key>K*} w + need * w(K*), so the normalised
+// weights are written in the same pass that compacts the indices.
+constexpr int kLdsKeys = 35 * 1024;
+constexpr int kSubHist = 4;
+constexpr int kBins = kSubHist * 256;  // value-linear bins of the boundary search (one per thread)
+static_assert(kBins == kTopkThreads, "one boundary bin per thread");
+
+// Non-decreasing in x; NaN products (inf - inf, 0 * inf) fall in bin 0, so the index is
+// always in range.
+__device__ __forceinline__ int value_bin(float x, float mn, float inv) {
+  const float b = (x - mn) * inv;
+  if (!(b > 0.0f)) return 0;
+  return b >= static_cast<float>(kBins - 1) ? kBins - 1 : static_cast<int>(b);
+}
+
+struct LdsShared {
+  uint32_t keys[kLdsKeys];
+  uint32_t hist[kSubHist][256];
+  uint32_t wave_cnt[kTopkWaves];
+  uint32_t wave_cnt2[kTopkWaves];
+  float red[kTopkWaves];
+  uint32_t sel_digit;
+  uint32_t bin_above;
+};
+
+__device__ float lds_block_max(float v, LdsShared& sh) {
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh.red[0];
+#pragma unroll
+  for (int i = 1; i < kTopkWaves; ++i) r = fmaxf(r, sh.red[i]);
+  return r;
+}
+
+__device__ float lds_block_sum(float v, LdsShared& sh) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kTopkWaves; ++i) r += sh.red[i];
+  return r;
+}
+
+__global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const float* scores, int64_t stride,
+                                                                       const int32_t* n_keys, int rows_per_count,
+                                                                       double fraction, int cap, int32_t* indices,
+                                                                       uint8_t* valid, float* mass, float* weights,
+                                                                       int32_t* counts) {
+  __shared__ LdsShared sh;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const float* x = scores + static_cast<int64_t>(r) * stride;
+  int n = min(n_keys[r / rows_per_count], static_cast<int>(min<int64_t>(stride, 0x7fffffff)));
+  n = min(n, kLdsKeys);
+  int32_t* oi = indices + static_cast<int64_t>(r) * cap;
+  uint8_t* ov = valid + static_cast<int64_t>(r) * cap;
+  float* ow = weights + static_cast<int64_t>(r) * cap;
+  int k = 0;
+  if (n > 0) {
+    const double want = ceil(static_cast<double>(n) * fraction);
+    k = static_cast<int>(want < 1.0 ? 1.0 : want);
+    if (k > n) k = n;
+  }
+  if (k > cap) k = cap;
+  for (int j = k + tid; j < cap; j += kTopkThreads) {
+    oi[j] = 0;
+    ov[j] = 0;
+    ow[j] = 0.0f;
+  }
+  if (k == 0) {
+    if (tid == 0) {
+      mass[r] = 0.0f;
+      if (counts) counts[r] = 0;
+    }
+    return;
+  }
+  float mx = -INFINITY;
+  // all of this thread's loads are issued before the first is used
+  constexpr int kPer = kLdsKeys / kTopkThreads;
+  float xs[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * kTopkThreads + tid;
+    xs[j] = (i < n) ? x[i] : -INFINITY;
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * kTopkThreads + tid;
+    if (i < n) {
+      sh.keys[i] = order_key(xs[j]);
+      mx = fmaxf(mx, xs[j]);
+    }
+  }
+  const float M = lds_block_max(mx, sh);  // (its barriers also publish sh.keys)
+  float z = 0.0f;
+  for (int i = tid; i < n; i += kTopkThreads) z += fast_exp2((key_value(sh.keys[i]) - M) * kLog2e);
+  const float Z = lds_block_sum(z, sh);
+
+  // ---- boundary bin: histogram of the scores over kBins value-linear bins.  The bin
+  // is a non-decreasing function of the score, so the k-th largest key lies in the bin
+  // where the count from the top reaches k, and every key of a higher bin is larger.
+  float mn = 1e30f;
+  for (int i = tid; i < n; i += kTopkThreads) mn = fminf(mn, key_value(sh.keys[i]));
+  mn = -lds_block_max(-mn, sh);
+  // non-finite extremes collapse every key into bin 0 (the radix select then covers all)
+  const float inv = (isfinite(M) && isfinite(mn) && M > mn) ? static_cast<float>(kBins) / (M - mn) : 0.0f;
+  uint32_t* lin = &sh.hist[0][0];  // kBins == kSubHist * 256 counters
+  for (int i = tid; i < kBins; i += kTopkThreads) lin[i] = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += kTopkThreads) atomicAdd(&lin[value_bin(key_value(sh.keys[i]), mn, inv)], 1u);
+  __syncthreads();
+  {
+    // descending inclusive scan over bins: thread t owns bin kBins-1-t
+    const int bin = kBins - 1 - tid;
+    const uint32_t h = lin[bin];
+    uint32_t incl = h;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += o;
+    }
+    if (lane == 63) sh.wave_cnt[w] = incl;
+    __syncthreads();
+    uint32_t base = 0;
+    for (int q = 0; q < w; ++q) base += sh.wave_cnt[q];
+    const uint32_t above = base + incl - h;
+    if (above < static_cast<uint32_t>(k) && above + h >= static_cast<uint32_t>(k)) {
+      sh.sel_digit = static_cast<uint32_t>(bin);
+      sh.bin_above = above;
+    }
+    __syncthreads();
+  }
+  const int bstar = static_cast<int>(sh.sel_digit);
+  const int above_bins = static_cast<int>(sh.bin_above);
+  __syncthreads();
+
+  // ---- radix select (8-bit digits, most significant first) among the keys of bin B*
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = k - above_bins;
+  uint32_t* hist = &sh.hist[w & (kSubHist - 1)][0];
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int i = tid; i < kSubHist * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += kTopkThreads) {
+      const uint32_t kk = sh.keys[i];
+      if ((kk & pmask) == prefix && value_bin(key_value(kk), mn, inv) == bstar)
+        atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
+    }
+    __syncthreads();
+    if (tid < kWave) {
+      uint32_t h[4];
+      uint32_t local = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int bin = 255 - 4 * lane - e;
+        h[e] = 0;
+#pragma unroll
+        for (int q = 0; q < kSubHist; ++q) h[e] += sh.hist[q][bin];
+        local += h[e];
+      }
+      uint32_t incl = local;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t o = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += o;
+      }
+      uint32_t above = incl - local;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (above < static_cast<uint32_t>(remaining) && above + h[e] >= static_cast<uint32_t>(remaining)) {
+          sh.sel_digit = 255 - 4 * lane - e;
+          sh.bin_above = above;
+        }
+        above += h[e];
+      }
+    }
+    __syncthreads();
+    prefix |= sh.sel_digit << shift;
+    pmask |= 0xFFu << shift;
+    remaining -= static_cast<int>(sh.bin_above);
+    __syncthreads();
+  }
+  const uint32_t kth = prefix;
+  const int need = remaining;
+
+  // ---- selected mass: keys above K* plus `need` copies of w(K*)
+  float wgt = 0.0f;
+  for (int i = tid; i < n; i += kTopkThreads) {
+    const uint32_t kk = sh.keys[i];
+    if (kk > kth) wgt += fast_exp2((key_value(kk) - M) * kLog2e);
+  }
+  const float Sgt = lds_block_sum(wgt, sh);
+  const float invZ = 1.0f / Z;
+  const float S = (Sgt + static_cast<float>(need) * fast_exp2((key_value(kth) - M) * kLog2e)) * invZ;
+  const float scale = invZ / S;
+
+  // ---- compaction in index order
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int eq_base = 0, out_base = 0;
+  for (int base = 0; base < n; base += kTopkThreads) {
+    const int i = base + tid;
+    const uint32_t kk = (i < n) ? sh.keys[i] : 0u;
+    const bool gt = i < n && kk > kth;
+    const bool eq = i < n && kk == kth;
+    const uint64_t eq_ballot = __ballot(eq);
+    if (lane == 0) sh.wave_cnt[w] = static_cast<uint32_t>(__popcll(eq_ballot));
+    __syncthreads();
+    int eq_rank = eq_base + __popcll(eq_ballot & lt_mask);
+    int eq_total = 0;
+#pragma unroll
+    for (int q = 0; q < kTopkWaves; ++q) {
+      const int c = static_cast<int>(sh.wave_cnt[q]);
+      if (q < w) eq_rank += c;
+      eq_total += c;
+    }
+    const bool sel = gt || (eq && eq_rank < need);
+    const uint64_t sel_ballot = __ballot(sel);
+    if (lane == 0) sh.wave_cnt2[w] = static_cast<uint32_t>(__popcll(sel_ballot));
+    __syncthreads();
+    int pos = out_base + __popcll(sel_ballot & lt_mask);
+    int sel_total = 0;
+#pragma unroll
+    for (int q = 0; q < kTopkWaves; ++q) {
+      const int c = static_cast<int>(sh.wave_cnt2[q]);
+      if (q < w) pos += c;
+      sel_total += c;
+    }
+    if (sel && pos < cap) {
+      oi[pos] = i;
+      ov[pos] = 1;
+      ow[pos] = fast_exp2((key_value(kk) - M) * kLog2e) * scale;
+    }
+    eq_base += eq_total;
+    out_base += sel_total;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    mass[r] = S;
+    if (counts) counts[r] = k;
+  }
+}
+
 struct EligibleCand {
   const uint8_t* elig;
   int last;  // excluded index (forced), or -1
@@ -321,8 +573,15 @@ extern "C" int32_t fl_decode_topk(const float* scores, int64_t scores_stride, in
   FL_REQUIRE(fraction > 0.0 && fraction <= 1.0, "fl_decode_topk: fraction must be in (0, 1]");
   FL_REQUIRE(scores_stride > 0, "fl_decode_topk: bad stride");
   if (rows == 0) return FL_OK;
-  hipLaunchKernelGGL(decode_topk_kernel, dim3(rows), dim3(kTopkThreads), 0, static_cast<hipStream_t>(stream), scores,
-                     scores_stride, n_keys, rows_per_count, fraction, capacity, indices, valid, mass, weights, counts);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(rows), block(kTopkThreads);  // block: fallback kernel
+  // the stride bounds every row's key count: rows that fit in LDS take the one-read kernel
+  if (scores_stride <= kLdsKeys)
+    hipLaunchKernelGGL(decode_topk_lds_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+                       fraction, capacity, indices, valid, mass, weights, counts);
+  else
+    hipLaunchKernelGGL(decode_topk_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+                       fraction, capacity, indices, valid, mass, weights, counts);
   FL_LAUNCH_CHECK("fl_decode_topk");
   return FL_OK;
 }

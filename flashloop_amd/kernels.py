@@ -62,15 +62,15 @@ def pack_kv_groups(view, loops, src_keys, src_values, *, src_bh_stride, src_row_
 
 # ---------------------------------------------------------------------------- J2
 class Workspace:
-    """Grow-only device scratch reused across calls (the reference keeps per-layer
-    split-KV workspaces the same way, flashloop/cache.py:672-704)."""
+    """Grow-only device scratch reused across calls ordered on one stream (the reference
+    keeps per-layer split-KV workspaces the same way, flashloop/cache.py:672-704)."""
 
     def __init__(self) -> None:
         self._buf: torch.Tensor | None = None
 
     def get(self, nbytes: int, device) -> torch.Tensor:
         if self._buf is None or self._buf.numel() < nbytes or self._buf.device != torch.device(device):
-            self._buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            self._buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         return self._buf
 
 
@@ -170,6 +170,36 @@ def fused_sparse_attention_delta(view, loop, query, current_key, current_value, 
                                          ws.numel(), _stream())
     check(rc, "fl_decode_attn_sparse_delta")
     return out
+
+
+def fused_sparse_attention_delta_with_source(view, loop, query, current_key, current_value, indices, valid,
+                                             source_weights, source_current_value, global_mass, scaling, *,
+                                             device, workspace: Workspace | None = None):
+    """Loop-3/4 cached-mass delta that also forms the loop-2 selected aggregate from the
+    rows it reads.  Returns (delta f32 [B*H,128], source_output f32 [B*H,128])."""
+    lib = load()
+    rows = view.batch * view.heads
+    cap = indices.shape[-1]
+    indices = indices.reshape(rows, cap)
+    valid = valid.reshape(rows, cap)
+    weights = source_weights.reshape(rows, cap)
+    _require(indices, torch.int32, "indices")
+    _require(valid, torch.uint8, "valid")
+    _require(weights, torch.float32, "source_weights")
+    mass = global_mass.reshape(rows).float().contiguous()
+    q = _vec(query, rows, "query")
+    kc = _vec(current_key, rows, "current_key")
+    vc = _vec(current_value, rows, "current_value")
+    vc1 = _vec(source_current_value, rows, "source_current_value")
+    out = torch.empty(rows, HEAD_DIM, dtype=torch.float32, device=device)
+    src = torch.empty(rows, HEAD_DIM, dtype=torch.float32, device=device)
+    ws = (workspace or _WS).get(lib.fl_decode_selected_workspace(C.byref(view), cap), device)
+    rc = lib.fl_decode_attn_sparse_delta_fused(C.byref(view), loop, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                               indices.data_ptr(), valid.data_ptr(), weights.data_ptr(),
+                                               vc1.data_ptr(), cap, mass.data_ptr(), float(scaling),
+                                               src.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+    check(rc, "fl_decode_attn_sparse_delta_fused")
+    return out, src
 
 
 # ---------------------------------------------------------------------------- J4

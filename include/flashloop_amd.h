@@ -124,7 +124,8 @@ int32_t fl_pack_kv_groups(const fl_cache_view* view, int32_t loops,
  * holding scaling*q.k for the packed_tokens[b] + tail_tokens[b] + 1 keys.
  * `loop` in 0..3 (the reference kernel supports 0..1; 2..3 serve
  * enable_sparse_decode=False, flashloop/engine.py:422).
- * workspace: fl_decode_attn_dense_workspace() bytes, any content.
+ * workspace: fl_decode_attn_dense_workspace() bytes (16-byte aligned, any content) for the
+ * per-split partials; calls that share a workspace must be ordered on one stream.
  */
 size_t fl_decode_attn_dense_workspace(const fl_cache_view* view);
 int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
@@ -161,6 +162,8 @@ int32_t fl_decode_topk(const float* scores, int64_t scores_stride, int32_t rows,
  *   out[bh] = sum_j valid*weights[bh,j] * V_loop[indices[bh,j]],
  * where index packed_tokens[b]+tail_tokens[b] is the current token (v_cur).
  * indices/valid/weights: [B*H, capacity].  out f32 [B*H, 128].
+ * workspace: fl_decode_selected_workspace() bytes, with the same contract as
+ * fl_decode_attn_dense.
  */
 size_t fl_decode_selected_workspace(const fl_cache_view* view, int32_t capacity);
 int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop, const int32_t* indices,
@@ -186,6 +189,25 @@ int32_t fl_decode_attn_sparse_delta(const fl_cache_view* view, int32_t loop,
                                     const float* source_output, const float* mass,
                                     float scaling, float* out,
                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * J2 (sparse, fused) -- fl_decode_attn_sparse_delta that also forms its source_output.
+ *
+ * Same result as fl_decode_selected_pv(loop=1, source_weights, source_v_cur) followed by
+ * fl_decode_attn_sparse_delta(loop, ...), in one pass over the selected rows: the
+ * loop-`loop` reader already loads V streams 0 and 1 of every selected row, which is
+ * all the loop-2 aggregate needs (flashloop/engine.py:346-371 computes it at loop 2
+ * and consumes it at loops 3 and 4, engine.py:511-528).  source_output f32 [B*H,128]
+ * receives the aggregate for reuse by the loop-4 call.  loop must be 2 or 3.
+ */
+int32_t fl_decode_attn_sparse_delta_fused(const fl_cache_view* view, int32_t loop,
+                                          const uint16_t* q, const uint16_t* k_cur,
+                                          const uint16_t* v_cur, const int32_t* indices,
+                                          const uint8_t* valid, const float* source_weights,
+                                          const uint16_t* source_v_cur, int32_t capacity,
+                                          const float* mass, float scaling, float* source_output,
+                                          float* out, void* workspace, size_t workspace_bytes,
+                                          void* stream);
 
 /*
  * J4 -- token-sparse update row movement.

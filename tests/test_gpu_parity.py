@@ -171,7 +171,12 @@ def _step_vs_oracle(w, layer, m3=None, m4=None, frac=0.10):
     ks = [c[0].to(DEV) for c in cur]
     vs = [c[1].to(DEV) for c in cur]
     step = decode_attention_step(layer, qs, ks, vs, SCALING, frac)
+    unfused = decode_attention_step(layer, qs, ks, vs, SCALING, frac, fused_source=False)
     torch.cuda.synchronize()
+    # the fused loop-3 pass forms the same loop-2 aggregate as the separate selected-PV pass
+    for a_, b_ in ((step.selected_output, unfused.selected_output), (step.delta2, unfused.delta2),
+                   (step.delta3, unfused.delta3)):
+        assert torch.allclose(a_, b_, atol=1e-5, rtol=1e-5)
     lengths = [x for x in w.lengths for _ in range(h)]
     q = [np32(w.queries[r]).reshape(R, 128) for r in range(4)]
     kc = [np32(c[0]).reshape(R, 128) for c in cur]
