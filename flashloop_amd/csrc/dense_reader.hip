@@ -35,6 +35,8 @@ struct DenseArgs {
   int64_t logits_stride;
   float* ws;  // [B*H, nsplit+1, kPartial]
   float* out;
+  const uint16_t* tail_k;  // tail_key[loop] / tail_value[loop], resolved on the host
+  const uint16_t* tail_v;
   int nsplit;
   int gps;    // groups per prefix split
 };

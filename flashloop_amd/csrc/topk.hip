@@ -231,13 +231,23 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
 }
 
 // LDS-resident variant for rows of at most kLdsKeys keys (gfx950: 160 KiB of LDS per
-// workgroup): the row is read from HBM once into LDS as order-preserving keys; the
-// radix passes and the compaction read LDS.  Histograms are split four ways to spread
-// LDS atomics.  The selected mass is sum_{key>K*} w + need * w(K*), so the normalised
-// weights are written in the same pass that compacts the indices.
+// workgroup).  Passes over the row:
+//   1. load from HBM into LDS as order-preserving keys (all loads issued first);
+//   2. softmax normaliser and a histogram over kBins value-linear bins -- the bin is a
+//      non-decreasing function of the score, so the k-th largest key lies in the bin B*
+//      where the count from the top reaches k, and every key of a higher bin is larger;
+//   3. the keys of B* (a few dozen for smooth score distributions) are compacted into an
+//      LDS list and ranked there by (score desc, index asc), which fixes the k-th key
+//      (kth_key, kth_idx) -- a bin too crowded for the list falls back to an exact radix
+//      select restricted to B*;
+//   4. the selected keys (key > kth_key, or key == kth_key and index <= kth_idx) are
+//      written in index order: per (chunk, wave) ballot counts, one prefix scan, then
+//      each lane writes at its offset.
 constexpr int kLdsKeys = 35 * 1024;
+constexpr int kPer = kLdsKeys / kTopkThreads;
 constexpr int kSubHist = 4;
 constexpr int kBins = kSubHist * 256;  // value-linear bins of the boundary search (one per thread)
+constexpr int kCand = 512;             // boundary-bin list capacity
 static_assert(kBins == kTopkThreads, "one boundary bin per thread");
 
 // Non-decreasing in x; NaN products (inf - inf, 0 * inf) fall in bin 0, so the index is
@@ -251,11 +261,15 @@ __device__ __forceinline__ int value_bin(float x, float mn, float inv) {
 struct LdsShared {
   uint32_t keys[kLdsKeys];
   uint32_t hist[kSubHist][256];
-  uint32_t wave_cnt[kTopkWaves];
-  uint32_t wave_cnt2[kTopkWaves];
+  uint32_t cnt[kPer][kTopkWaves];  // per (chunk, wave) counts, then their exclusive prefix
+  uint32_t cand_key[kCand];
+  uint32_t cand_idx[kCand];
   float red[kTopkWaves];
   uint32_t sel_digit;
   uint32_t bin_above;
+  uint32_t ncand;
+  uint32_t kth_key;
+  uint32_t kth_idx;
 };
 
 __device__ float lds_block_max(float v, LdsShared& sh) {
@@ -280,6 +294,42 @@ __device__ float lds_block_sum(float v, LdsShared& sh) {
   return r;
 }
 
+// Exclusive prefix of sh.cnt in index order (chunk-major, wave-minor), done by wave 0;
+// returns the total.  Caller brackets it with barriers.
+__device__ uint32_t prefix_counts(LdsShared& sh) {
+  __shared__ uint32_t total;
+  if (threadIdx.x < kWave) {
+    const int lane = threadIdx.x;
+    constexpr int kN = kPer * kTopkWaves;
+    constexpr int kEach = (kN + kWave - 1) / kWave;
+    uint32_t* c = &sh.cnt[0][0];
+    uint32_t loc[kEach];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int e = 0; e < kEach; ++e) {
+      const int i = lane * kEach + e;
+      loc[e] = i < kN ? c[i] : 0u;
+      sum += loc[e];
+    }
+    uint32_t incl = sum;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t o = __shfl_up(incl, off, kWave);
+      if (lane >= off) incl += o;
+    }
+    uint32_t run = incl - sum;
+#pragma unroll
+    for (int e = 0; e < kEach; ++e) {
+      const int i = lane * kEach + e;
+      if (i < kN) c[i] = run;
+      run += loc[e];
+    }
+    if (lane == kWave - 1) total = incl;
+  }
+  __syncthreads();
+  return total;
+}
+
 __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const float* scores, int64_t stride,
                                                                        const int32_t* n_keys, int rows_per_count,
                                                                        double fraction, int cap, int32_t* indices,
@@ -288,6 +338,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
   __shared__ LdsShared sh;
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const float* x = scores + static_cast<int64_t>(r) * stride;
   int n = min(n_keys[r / rows_per_count], static_cast<int>(min<int64_t>(stride, 0x7fffffff)));
   n = min(n, kLdsKeys);
@@ -313,44 +364,44 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
     }
     return;
   }
-  float mx = -INFINITY;
-  // all of this thread's loads are issued before the first is used
-  constexpr int kPer = kLdsKeys / kTopkThreads;
-  float xs[kPer];
+
+  // ---- 1. load
+  float mx = -INFINITY, mn = INFINITY;
+  {
+    float xs[kPer];
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = j * kTopkThreads + tid;
-    xs[j] = (i < n) ? x[i] : -INFINITY;
-  }
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * kTopkThreads + tid;
+      xs[j] = (i < n) ? x[i] : 0.0f;
+    }
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = j * kTopkThreads + tid;
-    if (i < n) {
-      sh.keys[i] = order_key(xs[j]);
-      mx = fmaxf(mx, xs[j]);
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * kTopkThreads + tid;
+      if (i < n) {
+        sh.keys[i] = order_key(xs[j]);
+        mx = fmaxf(mx, xs[j]);
+        mn = fminf(mn, xs[j]);
+      }
     }
   }
-  const float M = lds_block_max(mx, sh);  // (its barriers also publish sh.keys)
-  float z = 0.0f;
-  for (int i = tid; i < n; i += kTopkThreads) z += fast_exp2((key_value(sh.keys[i]) - M) * kLog2e);
-  const float Z = lds_block_sum(z, sh);
-
-  // ---- boundary bin: histogram of the scores over kBins value-linear bins.  The bin
-  // is a non-decreasing function of the score, so the k-th largest key lies in the bin
-  // where the count from the top reaches k, and every key of a higher bin is larger.
-  float mn = 1e30f;
-  for (int i = tid; i < n; i += kTopkThreads) mn = fminf(mn, key_value(sh.keys[i]));
+  for (int i = tid; i < kBins; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
+  if (tid == 0) sh.ncand = 0;
+  const float M = lds_block_max(mx, sh);
   mn = -lds_block_max(-mn, sh);
-  // non-finite extremes collapse every key into bin 0 (the radix select then covers all)
+  // non-finite extremes collapse every key into bin 0 (the fallback then covers all)
   const float inv = (isfinite(M) && isfinite(mn) && M > mn) ? static_cast<float>(kBins) / (M - mn) : 0.0f;
-  uint32_t* lin = &sh.hist[0][0];  // kBins == kSubHist * 256 counters
-  for (int i = tid; i < kBins; i += kTopkThreads) lin[i] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += kTopkThreads) atomicAdd(&lin[value_bin(key_value(sh.keys[i]), mn, inv)], 1u);
-  __syncthreads();
+
+  // ---- 2. normaliser and value histogram
+  float z = 0.0f;
+  uint32_t* lin = &sh.hist[0][0];  // one kBins-bin histogram (the sub-histograms are for the radix)
+  for (int i = tid; i < n; i += kTopkThreads) {
+    const float xi = key_value(sh.keys[i]);
+    z += fast_exp2((xi - M) * kLog2e);
+    atomicAdd(&lin[value_bin(xi, mn, inv)], 1u);
+  }
+  const float Z = lds_block_sum(z, sh);  // (its barriers also complete the histogram)
   {
-    // descending inclusive scan over bins: thread t owns bin kBins-1-t
-    const int bin = kBins - 1 - tid;
+    const int bin = kBins - 1 - tid;  // descending scan: thread t owns bin kBins-1-t
     const uint32_t h = lin[bin];
     uint32_t incl = h;
 #pragma unroll
@@ -358,10 +409,10 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
       const uint32_t o = __shfl_up(incl, off, kWave);
       if (lane >= off) incl += o;
     }
-    if (lane == 63) sh.wave_cnt[w] = incl;
+    if (lane == 63) sh.cnt[0][w] = incl;
     __syncthreads();
     uint32_t base = 0;
-    for (int q = 0; q < w; ++q) base += sh.wave_cnt[q];
+    for (int q = 0; q < w; ++q) base += sh.cnt[0][q];
     const uint32_t above = base + incl - h;
     if (above < static_cast<uint32_t>(k) && above + h >= static_cast<uint32_t>(k)) {
       sh.sel_digit = static_cast<uint32_t>(bin);
@@ -370,109 +421,138 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
     __syncthreads();
   }
   const int bstar = static_cast<int>(sh.sel_digit);
-  const int above_bins = static_cast<int>(sh.bin_above);
-  __syncthreads();
+  const int need_b = k - static_cast<int>(sh.bin_above);  // >= 1 keys of B* are selected
 
-  // ---- radix select (8-bit digits, most significant first) among the keys of bin B*
-  uint32_t prefix = 0, pmask = 0;
-  int remaining = k - above_bins;
-  uint32_t* hist = &sh.hist[w & (kSubHist - 1)][0];
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = tid; i < kSubHist * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += kTopkThreads) {
-      const uint32_t kk = sh.keys[i];
-      if ((kk & pmask) == prefix && value_bin(key_value(kk), mn, inv) == bstar)
-        atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
-    }
-    __syncthreads();
-    if (tid < kWave) {
-      uint32_t h[4];
-      uint32_t local = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int bin = 255 - 4 * lane - e;
-        h[e] = 0;
-#pragma unroll
-        for (int q = 0; q < kSubHist; ++q) h[e] += sh.hist[q][bin];
-        local += h[e];
-      }
-      uint32_t incl = local;
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const uint32_t o = __shfl_up(incl, off, kWave);
-        if (lane >= off) incl += o;
-      }
-      uint32_t above = incl - local;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if (above < static_cast<uint32_t>(remaining) && above + h[e] >= static_cast<uint32_t>(remaining)) {
-          sh.sel_digit = 255 - 4 * lane - e;
-          sh.bin_above = above;
-        }
-        above += h[e];
-      }
-    }
-    __syncthreads();
-    prefix |= sh.sel_digit << shift;
-    pmask |= 0xFFu << shift;
-    remaining -= static_cast<int>(sh.bin_above);
-    __syncthreads();
-  }
-  const uint32_t kth = prefix;
-  const int need = remaining;
-
-  // ---- selected mass: keys above K* plus `need` copies of w(K*)
-  float wgt = 0.0f;
+  // ---- 3. keys of the boundary bin -> (kth_key, kth_idx)
   for (int i = tid; i < n; i += kTopkThreads) {
     const uint32_t kk = sh.keys[i];
-    if (kk > kth) wgt += fast_exp2((key_value(kk) - M) * kLog2e);
+    if (value_bin(key_value(kk), mn, inv) == bstar) {
+      const uint32_t slot = atomicAdd(&sh.ncand, 1u);
+      if (slot < kCand) {
+        sh.cand_key[slot] = kk;
+        sh.cand_idx[slot] = static_cast<uint32_t>(i);
+      }
+    }
   }
-  const float Sgt = lds_block_sum(wgt, sh);
-  const float invZ = 1.0f / Z;
-  const float S = (Sgt + static_cast<float>(need) * fast_exp2((key_value(kth) - M) * kLog2e)) * invZ;
-  const float scale = invZ / S;
+  __syncthreads();
+  const int m = static_cast<int>(sh.ncand);
+  if (m <= kCand) {
+    if (tid < m) {
+      const uint32_t mk = sh.cand_key[tid], mi = sh.cand_idx[tid];
+      int rank = 0;
+      for (int u = 0; u < m; ++u) {
+        const uint32_t uk = sh.cand_key[u], ui = sh.cand_idx[u];
+        rank += (uk > mk || (uk == mk && ui < mi)) ? 1 : 0;
+      }
+      if (rank == need_b - 1) {
+        sh.kth_key = mk;
+        sh.kth_idx = mi;
+      }
+    }
+  } else {
+    // crowded bin (many equal or clustered scores): exact radix select within B*
+    uint32_t prefix = 0, pmask = 0;
+    int remaining = need_b;
+    uint32_t* hist = &sh.hist[w & (kSubHist - 1)][0];
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = tid; i < kSubHist * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
+      __syncthreads();
+      for (int i = tid; i < n; i += kTopkThreads) {
+        const uint32_t kk = sh.keys[i];
+        if ((kk & pmask) == prefix && value_bin(key_value(kk), mn, inv) == bstar)
+          atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
+      }
+      __syncthreads();
+      if (tid < kWave) {
+        uint32_t h[4];
+        uint32_t local = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int bin = 255 - 4 * lane - e;
+          h[e] = 0;
+#pragma unroll
+          for (int q = 0; q < kSubHist; ++q) h[e] += sh.hist[q][bin];
+          local += h[e];
+        }
+        uint32_t incl = local;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+          const uint32_t o = __shfl_up(incl, off, kWave);
+          if (lane >= off) incl += o;
+        }
+        uint32_t above = incl - local;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (above < static_cast<uint32_t>(remaining) && above + h[e] >= static_cast<uint32_t>(remaining)) {
+            sh.sel_digit = 255 - 4 * lane - e;
+            sh.bin_above = above;
+          }
+          above += h[e];
+        }
+      }
+      __syncthreads();
+      prefix |= sh.sel_digit << shift;
+      pmask |= 0xFFu << shift;
+      remaining -= static_cast<int>(sh.bin_above);
+      __syncthreads();
+    }
+    // the `remaining`-th key equal to `prefix` in index order is the k-th key
+#pragma unroll 1
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * kTopkThreads + tid;
+      const bool eq = i < n && sh.keys[i] == prefix;
+      const uint64_t bal = __ballot(eq);
+      if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
+    }
+    __syncthreads();
+    prefix_counts(sh);
+#pragma unroll 1
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * kTopkThreads + tid;
+      const bool eq = i < n && sh.keys[i] == prefix;
+      const uint64_t bal = __ballot(eq);
+      const int rank = static_cast<int>(sh.cnt[j][w]) + __popcll(bal & lt_mask);
+      if (eq && rank == remaining - 1) {
+        sh.kth_key = prefix;
+        sh.kth_idx = static_cast<uint32_t>(i);
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t kth_key = sh.kth_key;
+  const uint32_t kth_idx = sh.kth_idx;
 
-  // ---- compaction in index order
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int eq_base = 0, out_base = 0;
-  for (int base = 0; base < n; base += kTopkThreads) {
-    const int i = base + tid;
-    const uint32_t kk = (i < n) ? sh.keys[i] : 0u;
-    const bool gt = i < n && kk > kth;
-    const bool eq = i < n && kk == kth;
-    const uint64_t eq_ballot = __ballot(eq);
-    if (lane == 0) sh.wave_cnt[w] = static_cast<uint32_t>(__popcll(eq_ballot));
-    __syncthreads();
-    int eq_rank = eq_base + __popcll(eq_ballot & lt_mask);
-    int eq_total = 0;
-#pragma unroll
-    for (int q = 0; q < kTopkWaves; ++q) {
-      const int c = static_cast<int>(sh.wave_cnt[q]);
-      if (q < w) eq_rank += c;
-      eq_total += c;
-    }
-    const bool sel = gt || (eq && eq_rank < need);
-    const uint64_t sel_ballot = __ballot(sel);
-    if (lane == 0) sh.wave_cnt2[w] = static_cast<uint32_t>(__popcll(sel_ballot));
-    __syncthreads();
-    int pos = out_base + __popcll(sel_ballot & lt_mask);
-    int sel_total = 0;
-#pragma unroll
-    for (int q = 0; q < kTopkWaves; ++q) {
-      const int c = static_cast<int>(sh.wave_cnt2[q]);
-      if (q < w) pos += c;
-      sel_total += c;
-    }
+  // ---- 4. selected keys in index order
+#pragma unroll 1
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * kTopkThreads + tid;
+    const uint32_t kk = i < n ? sh.keys[i] : 0u;
+    const bool sel = i < n && (kk > kth_key || (kk == kth_key && static_cast<uint32_t>(i) <= kth_idx));
+    const uint64_t bal = __ballot(sel);
+    if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
+  }
+  __syncthreads();
+  prefix_counts(sh);
+  float msum = 0.0f;
+  const float invZ = 1.0f / Z;
+#pragma unroll 1
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * kTopkThreads + tid;
+    const uint32_t kk = i < n ? sh.keys[i] : 0u;
+    const bool sel = i < n && (kk > kth_key || (kk == kth_key && static_cast<uint32_t>(i) <= kth_idx));
+    const uint64_t bal = __ballot(sel);
+    const int pos = static_cast<int>(sh.cnt[j][w]) + __popcll(bal & lt_mask);
     if (sel && pos < cap) {
+      const float wv = fast_exp2((key_value(kk) - M) * kLog2e) * invZ;
       oi[pos] = i;
       ov[pos] = 1;
-      ow[pos] = fast_exp2((key_value(kk) - M) * kLog2e) * scale;
+      ow[pos] = wv;
+      msum += wv;
     }
-    eq_base += eq_total;
-    out_base += sel_total;
-    __syncthreads();
   }
+  const float S = lds_block_sum(msum, sh);  // its barriers also order the weight writes
+  const float invS = 1.0f / S;
+  for (int j = tid; j < k; j += kTopkThreads) ow[j] *= invS;
   if (tid == 0) {
     mass[r] = S;
     if (counts) counts[r] = k;
