@@ -28,6 +28,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "int4 KV-residual decode attn µs/step + HBM GB/s (%peak) at 32K ctx, bs=8"
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch of the dense loop-2 reader (reader + merge kernels), measured with
+# rocprofv3 FETCH_SIZE (x2.0 calibration against a 1 GiB copy) + WRITE_SIZE on MI355X;
+# summary in profiles/decode_step_cfg3.md.
+MEASURED_TRAFFIC = {"cfg3": (1344.4 + 22.1) * 1e6}
 CONFIGS = {
     "cfg3": dict(batch=8, heads=16, tokens=32768, seed=3),
     "cfg1": dict(batch=1, heads=16, tokens=8192, seed=1),
@@ -217,7 +221,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(reader_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC.get(args.config),
             "algorithmic_bytes": parts["dense_loop2"],
             "avg_us": round(reader_ms * 1e3, 2),
         },
