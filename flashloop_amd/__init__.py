@@ -13,6 +13,9 @@ from .cache import (  # noqa: F401
     decode_attention_step,
     packed_prefix_tokens,
 )
+from .config import FlashLoopConfig  # noqa: F401
+from .engine import FlashLoopEngine  # noqa: F401
+from .hooks import flashloop  # noqa: F401
 
 __all__ = [
     "AttentionStep",
@@ -21,4 +24,7 @@ __all__ = [
     "LayerGeometry",
     "decode_attention_step",
     "packed_prefix_tokens",
+    "FlashLoopConfig",
+    "FlashLoopEngine",
+    "flashloop",
 ]

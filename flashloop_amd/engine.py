@@ -1,0 +1,327 @@
+"""Batch-one looped-decoder inference with the FlashLoop lazy updates on MI355X.
+
+Mirrors ``FlashLoopEngine`` (flashloop/engine.py:112-607): ``from_pretrained``,
+``prefill``, ``decode``, ``generate``, ``reset``, ``state``.  The three lazy updates run
+on this build's HIP kernels:
+
+* token-sparse prefill loops 3/4 -- row scores (``fl_hidden_delta_score``), nested global
+  top-k selection with the forced last token (``fl_select_tokens``) and row gather /
+  scatter of hidden states and K/V (``fl_gather_rows`` / ``fl_scatter_rows``);
+* the int4 anchor + residual cross-loop KV cache (``fl_pack_kv_groups``);
+* decode loops 1-2 dense over the packed cache (``fl_decode_attn_dense``), loop-2 key
+  selection (``fl_decode_topk``), loops 3-4 cached-mass sparse attention
+  (``fl_decode_attn_sparse_delta[_fused]``).
+
+Model GEMMs, norms and SDPA of the dense prefill loops are torch (hipBLASLt).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels
+from .cache import CrossLoopKVCache, CrossLoopKVLayer
+from .config import FlashLoopConfig, validate_ouro_model
+from .model import OuroConfig, OuroForCausalLM, apply_rope
+
+
+@dataclass(frozen=True)
+class PrefillReceipt:
+    """Row accounting of one prefill loop (flashloop/prefill.py:46-58)."""
+
+    loop: int
+    total_rows: int
+    active_rows: int
+
+
+@dataclass(frozen=True)
+class EngineState:
+    cache: CrossLoopKVCache
+    next_position: int
+    mask_loop3: torch.Tensor
+    mask_loop4: torch.Tensor
+    prefill_receipts: tuple[PrefillReceipt, ...]
+
+
+@dataclass(frozen=True)
+class PrefillOutput:
+    logits: torch.Tensor
+    state: EngineState
+
+
+@dataclass(frozen=True)
+class DecodeReceipt:
+    dense_attention_calls: int
+    sparse_attention_calls: int
+    dense_late_loop_calls: int
+    selected_keys_per_layer: tuple[int, ...]
+
+
+@dataclass(frozen=True)
+class DecodeOutput:
+    logits: torch.Tensor
+    state: EngineState
+    receipt: DecodeReceipt
+
+
+@dataclass
+class _LayerSource:
+    """Loop-2 state reused by loops 3/4 (flashloop/engine.py:49-56)."""
+
+    projected_output: torch.Tensor
+    indices: torch.Tensor
+    valid: torch.Tensor
+    global_mass: torch.Tensor
+    selected_weights: torch.Tensor
+    current_value: torch.Tensor
+    selected_output: torch.Tensor | None = None
+    count: int = 0
+
+
+def _budget(tokens: int, fraction: float) -> int:
+    return max(1, math.ceil(tokens * fraction))
+
+
+class FlashLoopEngine:
+    """FlashLoop inference over an Ouro-shaped looped decoder, batch one."""
+
+    def __init__(self, model: OuroForCausalLM, *, config: FlashLoopConfig | None = None) -> None:
+        validate_ouro_model(model)
+        self.model = model.eval()
+        self.config = config or FlashLoopConfig()
+        self.backbone = model.model
+        self.layers = model.model.layers
+        self._state: EngineState | None = None
+        self.observer: Callable[[str, dict], None] | None = None
+
+    @classmethod
+    def from_pretrained(cls, model_path: str, *, config: FlashLoopConfig | None = None,
+                        torch_dtype: torch.dtype = torch.bfloat16, device="cuda") -> "FlashLoopEngine":
+        """Load weights written by ``OuroForCausalLM.save_pretrained`` (flashloop/engine.py:134-150)."""
+        return cls(OuroForCausalLM.from_pretrained(model_path, dtype=torch_dtype, device=device), config=config)
+
+    @classmethod
+    def from_random_init(cls, model_config: OuroConfig, *, seed: int = 0, config: FlashLoopConfig | None = None,
+                         device="cuda") -> "FlashLoopEngine":
+        return cls(OuroForCausalLM.random_init(model_config, seed=seed, device=device), config=config)
+
+    @property
+    def state(self) -> EngineState:
+        if self._state is None:
+            raise RuntimeError("engine cache is not initialized")
+        return self._state
+
+    def reset(self) -> None:
+        self._state = None
+
+    # ------------------------------------------------------------------ prefill
+    def _qkv(self, attn, x: torch.Tensor, rows: int):
+        q = attn.q_proj(x).view(1, rows, -1, attn.head_dim).transpose(1, 2)
+        k = attn.k_proj(x).view(1, rows, -1, attn.head_dim).transpose(1, 2)
+        v = attn.v_proj(x).view(1, rows, -1, attn.head_dim).transpose(1, 2)
+        return q, k, v
+
+    def _dense_loop(self, hidden: torch.Tensor, cos, sin):
+        """``dense_prefill_loop`` (flashloop/prefill.py:275-304): every row, causal SDPA."""
+        t = hidden.shape[1]
+        keys, values = [], []
+        h = hidden
+        for layer in self.layers:
+            a = layer.self_attn
+            q, k, v = self._qkv(a, layer.input_layernorm(h), t)
+            q, k = apply_rope(q, k, cos, sin)
+            o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            o = a.o_proj(o.transpose(1, 2).reshape(1, t, -1))
+            h = h + layer.input_layernorm_2(o)
+            h = h + layer.post_attention_layernorm_2(layer.mlp(layer.post_attention_layernorm(h)))
+            keys.append(k.contiguous())
+            values.append(v.contiguous())
+        return self.backbone.norm(h), keys, values
+
+    def _sparse_loop(self, hidden: torch.Tensor, positions: torch.Tensor, prev_keys, prev_values, cos, sin):
+        """``sparse_prefill_loop`` (flashloop/prefill.py:122-272): only the active rows are
+        recomputed; their K/V replace the previous loop's rows of a composite cache."""
+        t = hidden.shape[1]
+        n = positions.numel()
+        h = hidden.clone()
+        cos_a = cos.index_select(1, positions.long())
+        sin_a = sin.index_select(1, positions.long())
+        qpos = positions.long()
+        allowed = torch.arange(t, device=h.device)[None, :] <= qpos[:, None]  # [n, T]
+        keys, values = [], []
+        for li, layer in enumerate(self.layers):
+            a = layer.self_attn
+            active, _ = kernels.gather_rows(h, positions, dim=1)
+            q, k, v = self._qkv(a, layer.input_layernorm(active), n)
+            q, k = apply_rope(q, k, cos_a, sin_a)
+            full_k = prev_keys[li].clone()
+            full_v = prev_values[li].clone()
+            kernels.scatter_rows_(full_k, positions, k.contiguous(), dim=2)
+            kernels.scatter_rows_(full_v, positions, v.contiguous(), dim=2)
+            o = F.scaled_dot_product_attention(q, full_k, full_v, attn_mask=allowed[None, None])
+            o = a.o_proj(o.transpose(1, 2).reshape(1, n, -1))
+            active = active + layer.input_layernorm_2(o)
+            active = active + layer.post_attention_layernorm_2(layer.mlp(layer.post_attention_layernorm(active)))
+            kernels.scatter_rows_(h, positions, active.contiguous(), dim=1)
+            keys.append(full_k)
+            values.append(full_v)
+        # final norm on the active rows only (flashloop/prefill.py:254-256)
+        act, _ = kernels.gather_rows(h, positions, dim=1)
+        kernels.scatter_rows_(h, positions, self.backbone.norm(act).contiguous(), dim=1)
+        return h, keys, values
+
+    def _select(self, current, previous, fraction, eligible=None):
+        score = kernels.hidden_delta_score(current, previous)
+        mask, positions, counts, err = kernels.select_tokens(score, fraction, eligible=eligible)
+        n = int(counts[0].item())  # prefill syncs once per loop boundary, as the reference does
+        return mask, positions[0, :n].contiguous(), score
+
+    @torch.inference_mode()
+    def prefill(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None, *,
+                decode_capacity: int | None = None,
+                stage_observer: Callable[[str], None] | None = None) -> PrefillOutput:
+        """``FlashLoopEngine.prefill`` (flashloop/engine.py:161-344)."""
+
+        def stage(name: str) -> None:
+            if stage_observer is not None:
+                stage_observer(name)
+
+        stage("start")
+        if self._state is not None:
+            raise RuntimeError("engine cache is already initialized; call reset()")
+        if input_ids.ndim != 2 or input_ids.shape[0] != 1:
+            raise ValueError("the engine supports batch size one")
+        t = int(input_ids.shape[1])
+        if t <= 0:
+            raise ValueError("prefill requires at least one prompt token")
+        if attention_mask is not None and (attention_mask.shape != input_ids.shape or not bool(attention_mask.bool().all())):
+            raise ValueError("padding is not supported by the batch-one engine")
+        dev = input_ids.device
+        hidden = self.backbone.embed_tokens(input_ids)
+        cos, sin = self.backbone.rotary_emb(hidden, torch.arange(t, device=dev)[None])
+        stage("inputs_ready")
+        h1, k1, v1 = self._dense_loop(hidden, cos, sin)
+        stage("loop1_dense")
+        h2, k2, v2 = self._dense_loop(h1, cos, sin)
+        stage("loop2_dense")
+        f3, f4 = self.config.effective_prefill_fractions
+        mask3, pos3, _ = self._select(h2, h1, f3)
+        n3 = pos3.numel()
+        h3, k3, v3 = self._sparse_loop(h2, pos3, k2, v2, cos, sin)
+        stage("loop3_sparse")
+        mask4, pos4, _ = self._select(h3, h2, f4, eligible=mask3)
+        n4 = pos4.numel()
+        h4, k4, v4 = self._sparse_loop(h3, pos4, k3, v3, cos, sin)
+        stage("loop4_sparse")
+        cap = t + (self.config.decode_capacity if decode_capacity is None else int(decode_capacity))
+        cache = CrossLoopKVCache(num_layers=len(self.layers))
+        for li in range(len(self.layers)):
+            cache.set_layer(li, CrossLoopKVLayer.from_prefill(
+                [k1[li], k2[li], k3[li], k4[li]], [v1[li], v2[li], v3[li], v4[li]],
+                mask_loop3=mask3, mask_loop4=mask4, token_capacity=cap))
+        stage("physical_cache_finalized")
+        receipts = (PrefillReceipt(1, t, t), PrefillReceipt(2, t, t), PrefillReceipt(3, t, n3), PrefillReceipt(4, t, n4))
+        self._state = EngineState(cache, t, mask3, mask4, receipts)
+        logits = self.model.lm_head(h4[:, -1]).float()
+        stage("logits_ready")
+        return PrefillOutput(logits=logits, state=self._state)
+
+    # ------------------------------------------------------------------ decode
+    @torch.inference_mode()
+    def decode(self, token_ids: torch.Tensor) -> DecodeOutput:
+        """``FlashLoopEngine.decode`` (flashloop/engine.py:373-570)."""
+        state = self.state
+        if token_ids.shape != (1, 1):
+            raise ValueError("decode requires exactly one token at batch size one")
+        cfg = self.config
+        sparse = cfg.enable_sparse_decode
+        fraction = cfg.effective_decode_key_fraction
+        h = self.backbone.embed_tokens(token_ids)
+        pos = state.next_position
+        cos, sin = self.backbone.rotary_emb(h, torch.tensor([[pos]], device=h.device))
+        nl = len(self.layers)
+        cur_k = [[None] * 4 for _ in range(nl)]
+        cur_v = [[None] * 4 for _ in range(nl)]
+        sources: list[_LayerSource | None] = [None] * nl
+        counts: list[int] = []
+        for loop in range(4):
+            for li, layer in enumerate(self.layers):
+                a = layer.self_attn
+                residual = h
+                q, k, v = self._qkv(a, layer.input_layernorm(h), 1)
+                q, k = apply_rope(q, k, cos, sin)
+                q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+                cur_k[li][loop] = k
+                cur_v[li][loop] = v
+                lc = state.cache.layers[li]
+                if loop < 2 or not sparse:
+                    out, lg = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
+                                                        scaling=a.scaling, return_logits=(loop == 1 and sparse))
+                    projected = a.o_proj(out.to(q.dtype).transpose(1, 2).reshape(1, 1, -1))
+                    if loop == 1 and sparse:
+                        idx, valid, mass, w, cnt = lc.select_decode_keys(lg, fraction)
+                        sources[li] = _LayerSource(projected, idx, valid, mass, w, v,
+                                                   count=min(pos + 1, _budget(pos + 1, fraction)))
+                        counts.append(sources[li].count)
+                else:
+                    src = sources[li]
+                    if src.selected_output is None:
+                        delta, so = lc.cached_mass_sparse_attention_delta_with_source(
+                            loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
+                            source_weights=src.selected_weights, source_current_value=src.current_value,
+                            global_mass=src.global_mass, scaling=a.scaling)
+                        src.selected_output = so
+                    else:
+                        delta = lc.cached_mass_sparse_attention_delta(
+                            loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
+                            source_selected_output=src.selected_output, global_mass=src.global_mass,
+                            scaling=a.scaling)
+                    projected = src.projected_output + a.o_proj(delta.to(v.dtype).transpose(1, 2).reshape(1, 1, -1))
+                h = residual + layer.input_layernorm_2(projected)
+                h = h + layer.post_attention_layernorm_2(layer.mlp(layer.post_attention_layernorm(h)))
+            h = self.backbone.norm(h)
+        for li in range(nl):
+            state.cache.layers[li].append_decode_token(cur_k[li], cur_v[li])
+        self._state = EngineState(state.cache, pos + 1, state.mask_loop3, state.mask_loop4, state.prefill_receipts)
+        logits = self.model.lm_head(h[:, -1]).float()
+        receipt = DecodeReceipt(
+            dense_attention_calls=(2 if sparse else 4) * nl,
+            sparse_attention_calls=(2 if sparse else 0) * nl,
+            dense_late_loop_calls=(0 if sparse else 2) * nl,
+            selected_keys_per_layer=tuple(counts),
+        )
+        return DecodeOutput(logits=logits, state=self._state, receipt=receipt)
+
+    # ------------------------------------------------------------------ generate
+    @torch.inference_mode()
+    def generate(self, input_ids: torch.Tensor, *, max_new_tokens: int, eos_token_id: int | None = None,
+                 stop_token_sequences: tuple[tuple[int, ...], ...] = ()) -> torch.Tensor:
+        """Greedy generation (flashloop/engine.py:572-607).  The host reads each token back
+        only when an EOS id or stop sequence has to be checked."""
+        if int(max_new_tokens) <= 0:
+            raise ValueError("max_new_tokens must be positive")
+        if eos_token_id is None:
+            eos_token_id = getattr(self.model.config, "eos_token_id", None)
+        prefill = self.prefill(input_ids, decode_capacity=int(max_new_tokens) + 64)
+        generated = [input_ids]
+        logits = prefill.logits
+        completion: list[int] = []
+        check = eos_token_id is not None or bool(stop_token_sequences)
+        for step in range(int(max_new_tokens)):
+            nxt = torch.argmax(logits, dim=-1, keepdim=True)
+            generated.append(nxt)
+            if check:
+                completion.append(int(nxt.item()))
+                if eos_token_id is not None and completion[-1] == int(eos_token_id):
+                    break
+                if any(seq and len(completion) >= len(seq) and tuple(completion[-len(seq):]) == seq
+                       for seq in stop_token_sequences):
+                    break
+            if step + 1 < int(max_new_tokens):
+                logits = self.decode(nxt).logits
+        return torch.cat(generated, dim=1)

@@ -1,0 +1,105 @@
+"""End-to-end FlashLoopEngine on the HIP kernels (tiny random-init Ouro-shaped model)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.tokens import select_active_mask
+
+pytestmark = pytest.mark.gpu
+
+from flashloop_amd import kernels  # noqa: E402
+from flashloop_amd.config import FlashLoopConfig  # noqa: E402
+from flashloop_amd.engine import FlashLoopEngine  # noqa: E402
+from flashloop_amd.hooks import flashloop  # noqa: E402
+from flashloop_amd.model import OuroConfig, OuroForCausalLM  # noqa: E402
+
+TINY = OuroConfig(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                  num_attention_heads=2, num_key_value_heads=2)
+
+
+def _ids(t, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, TINY.vocab_size, (1, t), generator=g).cuda()
+
+
+def _cos(a, b):
+    return float(torch.nn.functional.cosine_similarity(a.flatten().double(), b.flatten().double(), dim=0))
+
+
+def test_prefill_all_rows_matches_dense_forward():
+    """With both prefill fractions 1.0 the token-sparse loops recompute every row, so the
+    prefill logits are the dense looped model's (gather/scatter + masked SDPA path)."""
+    model = OuroForCausalLM.random_init(TINY, seed=2, device="cuda")
+    eng = FlashLoopEngine(model, config=FlashLoopConfig(prefill_fraction_loop3=1.0, prefill_fraction_loop4=1.0))
+    ids = _ids(150)
+    out = eng.prefill(ids)
+    ref = model.dense_forward(ids)
+    assert torch.isfinite(out.logits).all()
+    assert (out.logits - ref).abs().max().item() < 5e-2 * max(1.0, ref.abs().max().item())
+    assert [r.active_rows for r in out.state.prefill_receipts] == [150, 150, 150, 150]
+
+
+def test_prefill_masks_match_oracle():
+    model = OuroForCausalLM.random_init(TINY, seed=4, device="cuda")
+    eng = FlashLoopEngine(model)
+    ids = _ids(200, seed=4)
+    seen = {}
+    orig = eng._select
+
+    def spy(cur, prev, fraction, eligible=None):
+        mask, pos, score = orig(cur, prev, fraction, eligible)
+        seen.setdefault("calls", []).append((score.float().cpu().numpy(), fraction,
+                                             None if eligible is None else eligible.cpu().numpy(),
+                                             mask.cpu().numpy(), pos.cpu().numpy()))
+        return mask, pos, score
+
+    eng._select = spy
+    st = eng.prefill(ids).state
+    assert len(seen["calls"]) == 2
+    for score, frac, el, mask, pos in seen["calls"]:
+        want = select_active_mask(score, frac, eligible=el)
+        np.testing.assert_array_equal(mask, want)
+        np.testing.assert_array_equal(pos, np.nonzero(want[0])[0])
+    assert [r.active_rows for r in st.prefill_receipts] == [200, 200, 50, 20]
+    assert bool(torch.all(~st.mask_loop4 | st.mask_loop3))
+    assert bool(st.mask_loop3[0, -1]) and bool(st.mask_loop4[0, -1])
+
+
+def test_decode_tracks_dense_model():
+    """Decode logits through the packed int4 cache stay close to the dense looped model
+    on the same tokens (cosine), with all keys selected so only the codec differs."""
+    model = OuroForCausalLM.random_init(TINY, seed=5, device="cuda")
+    eng = FlashLoopEngine(model, config=FlashLoopConfig(prefill_fraction_loop3=1.0, prefill_fraction_loop4=1.0,
+                                                        decode_key_fraction=1.0))
+    ids = _ids(130, seed=5)
+    eng.prefill(ids[:, :128], decode_capacity=64)
+    for i in range(128, 130):
+        d = eng.decode(ids[:, i:i + 1])
+        ref = model.dense_forward(ids[:, :i + 1])
+        assert torch.isfinite(d.logits).all()
+        assert _cos(d.logits, ref) > 0.98
+    assert d.receipt.sparse_attention_calls == 2 * TINY.num_hidden_layers
+    assert d.state.next_position == 130
+
+
+def test_generate_crosses_rollover_and_hooks():
+    model = OuroForCausalLM.random_init(TINY, seed=6, device="cuda")
+    eng = FlashLoopEngine(model)
+    ids = _ids(190, seed=6)
+    out = eng.generate(ids, max_new_tokens=70)  # tail 62 -> rolls over one 64-token group
+    assert out.shape == (1, 260) and torch.equal(out[:, :190], ids)
+    lay = eng.state.cache.layers[0]
+    assert lay.quantized_tokens == 192
+    eng.reset()
+    with pytest.raises(RuntimeError):
+        _ = eng.state
+    with flashloop(model) as hooks:
+        out2 = model.generate(ids, max_new_tokens=70)
+        audit = hooks["kv"].audit()
+        joint = hooks["attention_and_prefill"].audit()
+    assert torch.equal(out, out2)
+    assert audit["status"] == "PASS" and audit["quantized_tokens"] == 192
+    assert joint["token_sparse_prefill"]["mask_nested"]
+    assert joint["attention"]["target_replacements"] == 2 * TINY.num_hidden_layers * 69
+    assert model.generate.__func__ is OuroForCausalLM.generate
