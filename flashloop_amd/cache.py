@@ -225,15 +225,18 @@ class CrossLoopKVLayer:
 
     # ------------------------------------------------------------------ readers
     def logits_capacity(self) -> int:
-        """Row stride of the logits buffer: covers the longest prefix plus the longest tail."""
-        return self.quantized_tokens + self.tail_tokens_max + 1
+        """Row stride of the logits buffer: covers the longest prefix plus the longest tail
+        and the current token, rounded up to 64 floats so that every row starts on a
+        256-byte boundary (the reader writes logits in whole, aligned cache lines)."""
+        n = self.quantized_tokens + self.tail_tokens_max + 1
+        return (n + 63) // 64 * 64
 
     def dense_source_attention(self, loop: int, *, query, current_key, current_value, scaling: float,
                                return_logits: bool):
         """``CrossLoopKVLayer.dense_source_attention`` (flashloop/cache.py:1644-1756).
 
-        Returns ``(out f32 [B,H,1,128], logits f32 [B,H,1,T+1] or None)``; for ragged
-        batches logits rows are valid up to each sequence's own ``T+1``."""
+        Returns ``(out f32 [B,H,1,128], logits f32 [B,H,1,C] or None)``: logits row entries
+        are valid up to each sequence's own ``T+1`` (C >= max T+1 is the padded stride)."""
         out, logits = kernels.fused_dense_source_attention(
             self.view(), int(loop), query, current_key, current_value, scaling, return_logits=return_logits,
             logits_capacity=self.logits_capacity(), device=self.device, workspace=self.workspace,

@@ -4,21 +4,20 @@
 // out     = softmax(logits) . V_loop  over [packed prefix ; BF16 tail ; current token]
 //
 // Layout of the work (one launch + a merge launch):
-//   grid.x = split index (nsplit prefix splits + 1 tail/current split), grid.y = (b,h).
-//   A prefix split owns `gps` consecutive 64-token groups.  Each wave takes one group
-//   per iteration; inside a wave, lane = 4*row + quarter: 16 token rows x 4 channel
-//   quarters (32 channels = one 16-byte load per stream per token).
+//   The packed prefixes of all (b,h) form one global sequence of 64-token groups
+//   ((b,h)-major).  The grid is persistent: each wave of kPersistBlocks x 4 waves takes
+//   one contiguous range of ceil(G / waves) groups and streams it with the next group's
+//   loads in flight, flushing a partial (m, l, acc[128]) whenever its range crosses into
+//   the next (b,h).  The BF16 tail + current token of each (b,h) is one extra wave task.
+//   A merge kernel combines each row's partials (contiguous slots, see partial_slot).
 //
 // Per-channel K metadata is factored out of the dot product: for group g and stream s,
-//   q . deq_s(K)[t] = sum_c (q_c*scale_{g,c}) * code_{t,c} + sum_c q_c*min_{g,c},
-// so a token costs one nibble convert and one FMA per channel per stream; the
-// q*scale products and the min term are built once per group per wave in LDS.
-// Likewise V (per-token metadata) is accumulated as
+//   q . deq_s(K)[t] = sum_c (q_c*scale_{g,c}) * code_{t,c} + sum_c q_c*min_{g,c};
+// V (per-token metadata) likewise:
 //   sum_t p_t*(scale_t*code_t,c + min_t) = sum_t (p_t*scale_t)*code_t,c + sum_t p_t*min_t.
-// Each 4-lane quad keeps its own online-softmax state; the 64 quad states of a
-// workgroup are merged through LDS at the end of the split, and the splits of a row by
-// a second kernel.  No MFMA: one query per head makes this a GEMV, bound by HBM.
 #include "reader_common.h"
+
+#include <mutex>
 
 namespace fl {
 namespace {
@@ -26,244 +25,684 @@ using namespace reader;
 
 struct DenseArgs {
   fl_cache_view v;
-  int loop;
   const uint16_t* q;
   const uint16_t* kc;
   const uint16_t* vc;
   float scaling;
   float* logits;
   int64_t logits_stride;
-  float* ws;  // [B*H, nsplit+1, kPartial]
-  float* out;
+  float* ws;  // partial slots: [waves + B*H] prefix slots, then [B*H] tail slots
   const uint16_t* tail_k;  // tail_key[loop] / tail_value[loop], resolved on the host
   const uint16_t* tail_v;
-  int nsplit;
-  int gps;    // groups per prefix split
+  int waves;  // persistent waves in the grid
 };
 
-// Registers of one half-group (32 tokens, 2 per lane): K/V codes and V metadata of
-// every stream, plus (first half only) the group's K metadata for this lane's 2 channels.
-template <int NS>
-struct HalfSet {
-  float4 kmeta[NS];
-  uint4 kw[2][NS];
-  uint4 vw[2][NS];
-  float2 vm[2][NS];
-  bool has[2][NS];
-};
+// ---------------------------------------------------------------------------------
+// Global work sequence.  Row bh = b*H + h contributes kTailUnits units for its BF16 tail
+// (+ current token) followed by its G_b prefix groups, G_b = packed_tokens[b] / 64
+// (clamped to the capacity, so a bad length cannot fault).  Wave w owns units
+// [w*chunk, min((w+1)*chunk, U)), chunk = ceil(U / waves): it runs the tails whose first
+// unit it owns and streams the prefix groups it owns.  Counting a tail as kTailUnits
+// groups keeps the waves that also run tails from finishing last.  A wave's partial for
+// row bh goes to slot w + bh: the slots of one row are contiguous and disjoint from every
+// other row's.
+// ---------------------------------------------------------------------------------
+constexpr int kTailUnits = 4;
+constexpr int kLenCache = 1024;  // batches whose group counts are cached in LDS
 
-template <int NS>
-__device__ __forceinline__ void load_half(HalfSet<NS>& hs, const fl_cache_view& v, int bh, int b, int gi, int h,
-                                          int row, int quarter, int gcap) {
-  const int lane = threadIdx.x & 63;
-  if (h == 0) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      hs.kmeta[s] = *reinterpret_cast<const float4*>(
-          v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + gi) * kDim + 2 * lane) * 2);
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int t = gi * kGroup + row + 16 * (2 * h + i);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      int r = t;
-      if (s >= 2) r = v.rank[s - 2][static_cast<int64_t>(b) * v.token_capacity + t];
-      hs.has[i][s] = r >= 0 && r < v.row_capacity[s];
-      if (!hs.has[i][s]) r = 0;
-      const int64_t rowi = static_cast<int64_t>(bh) * v.row_capacity[s] + r;
-      hs.kw[i][s] = *reinterpret_cast<const uint4*>(v.key_codes[s] + rowi * kRowBytes + 16 * quarter);
-      hs.vw[i][s] = *reinterpret_cast<const uint4*>(v.value_codes[s] + rowi * kRowBytes + 16 * quarter);
-      hs.vm[i][s] = *reinterpret_cast<const float2*>(v.value_meta[s] + (rowi * 2 + (quarter >> 1)) * 2);
-    }
-  }
+__device__ __forceinline__ int row_groups(const fl_cache_view& v, int b) {
+  return max(min(v.packed_tokens[b], v.token_capacity), 0) / kGroup;
 }
 
-// Logits, online softmax and P.V for one half-group.  At h == 0 the group's q*scale
-// products (LDS, wave-private) and q.min constants are rebuilt from hs.kmeta.
-template <int NS>
-__device__ __forceinline__ void dense_half(HalfSet<NS>& hs, QuadState& st, const DenseArgs& a, const float* qf,
-                                           float (*qsh)[kDim], int b, int gi, int h, int row, int quarter,
-                                           float* lrow) {
-  const int lane = threadIdx.x & 63;
-  __shared__ float cs_sh[kWaves][4];
-  float* cs = cs_sh[threadIdx.x >> 6];
-  if (h == 0) {
-    const float q0 = qf[2 * lane], q1 = qf[2 * lane + 1];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      qsh[s][2 * lane] = q0 * hs.kmeta[s].x;
-      qsh[s][2 * lane + 1] = q1 * hs.kmeta[s].z * 0.0625f;  // odd channel: high nibble reads 16*code
-      const float c = wave_sum(fmaf(q0, hs.kmeta[s].y, q1 * hs.kmeta[s].w));
-      if (lane == 0) cs[s] = c;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// Group counts per batch: from LDS for the first kLenCache batches (no global load in
+// the streaming loop), from the length array beyond.
+struct RowLens {
+  const int* lds;
+  int n;
+  __device__ __forceinline__ int operator()(const fl_cache_view& v, int b) const {
+    return b < n ? lds[b] : row_groups(v, b);
   }
-  float lg[2] = {0.0f, 0.0f};
+};
+
+__device__ __forceinline__ int64_t total_units(const fl_cache_view& v, const RowLens& rl) {
+  int64_t u = 0;
+  for (int b = 0; b < v.batch; ++b) u += static_cast<int64_t>(v.heads) * (kTailUnits + rl(v, b));
+  return u;
+}
+
+__device__ __forceinline__ int64_t chunk_of(int64_t U, int waves) { return (U + waves - 1) / waves; }
+
+// Position in the work sequence: row (b, h), group gi of gb, row's first unit vs.
+struct Cursor {
+  int b, h, gi, gb;
+  int64_t vs;
+};
+
+// Row containing unit u; gi = u's offset within the row's units.
+__device__ __forceinline__ Cursor locate(const fl_cache_view& v, const RowLens& rl, int64_t u) {
+  Cursor c{0, 0, 0, 0, 0};
+  int64_t base = 0;
+  for (int b = 0; b < v.batch; ++b) {
+    const int gb = rl(v, b);
+    const int64_t span = kTailUnits + gb;
+    const int64_t all = static_cast<int64_t>(v.heads) * span;
+    if (u < base + all) {
+      c.b = b;
+      c.gb = gb;
+      c.h = static_cast<int>((u - base) / span);
+      c.vs = base + c.h * span;
+      c.gi = static_cast<int>(u - c.vs);
+      return c;
+    }
+    base += all;
+  }
+  c.b = v.batch;
+  c.vs = base;
+  return c;
+}
+
+__device__ __forceinline__ void next_row(Cursor& c, const fl_cache_view& v, const RowLens& rl) {
+  c.vs += kTailUnits + c.gb;
+  c.gi = 0;
+  if (++c.h == v.heads) {
+    c.h = 0;
+    ++c.b;
+  }
+  c.gb = c.b < v.batch ? rl(v, c.b) : 0;
+}
+
+// Move to the next prefix group (skipping rows without groups); stops past the end.
+__device__ __forceinline__ void advance(Cursor& c, const fl_cache_view& v, const RowLens& rl) {
+  ++c.gi;
+  while (c.gi >= c.gb && c.b < v.batch) next_row(c, v, rl);
+}
+
+__host__ __device__ __forceinline__ int64_t partial_slot(int w, int bh) { return static_cast<int64_t>(w) + bh; }
+
+// ---------------------------------------------------------------------------------
+// Prefix groups on the matrix cores.
+//
+// Both contractions of a 64-token group run as v_mfma_i32_16x16x64_i8 with the nibble
+// codes as one operand and a fixed-point image of the float factors as the other:
+//   logits: B = K codes [channel x token] (a lane's 16-byte row quarter, split into its
+//           even-channel and odd-channel nibbles), A = q*scale per channel;
+//   P.V:    B = V codes [token x channel] (read transposed out of LDS with
+//           ds_read_b64_tr_b4), A = p*scale per token.
+// A float factor x of a group is scaled to X = x*2^24*127/max|x| and rounded to an int32
+// (|X| < 2^31); its four bytes, re-centred so every byte is a signed digit, are the four
+// A rows m&3 = 0..3 of one MFMA, so the four accumulator rows of a lane hold the digit
+// sums of one token (or channel) and sum_k 256^k * D_k rebuilds the dot product with a
+// relative error near 2^-25 of the group's largest term -- the fp32 level.
+// Per 64 tokens and stream this is 8 + 8 MFMAs instead of ~4.5k VALU operations.
+// ---------------------------------------------------------------------------------
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+
+constexpr float kFixScale = 127.0f * 16777216.0f;  // 127 * 2^24
+constexpr float kLazyRescale = 8.0f;              // rescale when the max grows by > e^8
+
+// Fixed-point digits of X (|X| < 2^31): bytes d0..d3 with X = sum_k d_k*256^k, each d_k
+// a signed byte (d0..d2 re-centred by 0x80, d3 the top byte of X + 0x808080).
+__device__ __forceinline__ uint32_t fix_digits(float x, float inv) {
+  const int32_t X = static_cast<int32_t>(rintf(x * inv));
+  return (static_cast<uint32_t>(X) + 0x00808080u) ^ 0x00808080u;
+}
+
+__device__ __forceinline__ float undigit(const v4i& d) {
+  return fmaf(static_cast<float>(d[3]), 16777216.0f,
+              fmaf(static_cast<float>(d[2]), 65536.0f, fmaf(static_cast<float>(d[1]), 256.0f, static_cast<float>(d[0]))));
+}
+
+// 4x4 byte transpose inside each quad: lane q returns byte q of the four lanes' words.
+__device__ __forceinline__ uint32_t quad_byte_transpose(uint32_t x, int q) {
+  const uint32_t p1 = static_cast<uint32_t>(dpp_i<kDppXor1>(static_cast<int>(x)));
+  const uint32_t t = __builtin_amdgcn_perm(p1, x, (q & 1) ? 0x03070105u : 0x06020400u);
+  const uint32_t p2 = static_cast<uint32_t>(dpp_i<kDppXor2>(static_cast<int>(t)));
+  return __builtin_amdgcn_perm(p2, t, (q & 2) ? 0x03020706u : 0x05040100u);
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave-private LDS of the prefix path.
+template <int NS>
+struct PrefixLds {
+  uint4 vt[NS][256];          // V codes of the group: entry (i*64 + lane) = row 16i+(lane&15), quarter lane>>4
+  uint32_t y[NS][4][2][4][4];  // K-side digits [stream][digit][parity][quarter][4 words of 4 channels]
+  uint32_t z[NS][2][4][16];    // V-side digits [stream][half][digit][16 words of 4 tokens]
+};
+
+// One 64-token group of one wave: lane = 16*quarter + n.  K/V code loads cover rows
+// 16i+n (i = 0..3) at byte quarter `quarter`; V metadata is loaded for the lane's own
+// token (row = lane), K metadata for channels 2*lane, 2*lane+1, and q for the same two
+// channels (rows change along the global sequence).
+template <int NS>
+struct GroupSet {
+  float4 km[NS];
+  uint4 kw[4][NS];
+  float4 vm[NS];
+  uint4 vw[4][NS];
+  uint32_t qw;   // bf16 q of channels 2*lane, 2*lane+1
+  uint32_t has;  // stream s>=2: bit 5*(s-2)+i row present for tile i, bit 5*(s-2)+4 own token
+  int bh, gi;
+};
+
+template <int NS>
+__device__ __forceinline__ void load_group(GroupSet<NS>& gs, const DenseArgs& a, const Cursor& c) {
+  const fl_cache_view& v = a.v;
+  const int lane = threadIdx.x & 63, n = lane & 15, quarter = lane >> 4;
+  const int bh = c.b * v.heads + c.h, gi = c.gi;
+  const int gcap = v.token_capacity / kGroup;
+  int rows[NS][5];
+  uint32_t has = 0;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    float qe[16], qo[16];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float4 x = *reinterpret_cast<const float4*>(&qsh[s][32 * quarter + 8 * k]);
-      const float4 y = *reinterpret_cast<const float4*>(&qsh[s][32 * quarter + 8 * k + 4]);
-      qe[4 * k + 0] = x.x; qo[4 * k + 0] = x.y;
-      qe[4 * k + 1] = x.z; qo[4 * k + 1] = x.w;
-      qe[4 * k + 2] = y.x; qo[4 * k + 2] = y.y;
-      qe[4 * k + 3] = y.z; qo[4 * k + 3] = y.w;
-    }
-    const float c = cs[s];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      float d = 0.0f;
-      d = dot8(hs.kw[i][s].x, qe + 0, qo + 0, d);
-      d = dot8(hs.kw[i][s].y, qe + 4, qo + 4, d);
-      d = dot8(hs.kw[i][s].z, qe + 8, qo + 8, d);
-      d = dot8(hs.kw[i][s].w, qe + 12, qo + 12, d);
-      d = quad_sum(d) + c;
-      if (s < 2 || hs.has[i][s]) lg[i] += d;
+    for (int i = 0; i < 5; ++i) {
+      const int t = gi * kGroup + (i < 4 ? 16 * i + n : lane);
+      int r = t;
+      if (s >= 2) {
+        r = v.rank[s - 2][static_cast<int64_t>(c.b) * v.token_capacity + t];
+        const bool ok = r >= 0 && r < v.row_capacity[s];
+        if (ok) has |= 1u << (5 * (s - 2) + i);
+        else r = 0;
+      }
+      rows[s][i] = r;
     }
   }
-  if (lrow && quarter == 0) {
-    lrow[gi * kGroup + row + 16 * (2 * h)] = lg[0];
-    lrow[gi * kGroup + row + 16 * (2 * h + 1)] = lg[1];
-  }
-  float p[2];
-  online_update(st, lg, p, 2);
+  gs.has = has;
+  gs.bh = bh;
+  gs.gi = gi;
+  gs.qw = *reinterpret_cast<const uint32_t*>(a.q + static_cast<int64_t>(bh) * kDim + 2 * lane);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int s = 0; s < NS; ++s)
+    gs.km[s] = *reinterpret_cast<const float4*>(v.key_meta[s] +
+                                                ((static_cast<int64_t>(bh) * gcap + gi) * kDim + 2 * lane) * 2);
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      gs.kw[i][s] = *reinterpret_cast<const uint4*>(
+          v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][i]) * kRowBytes + 16 * quarter);
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    gs.vm[s] = *reinterpret_cast<const float4*>(v.value_meta[s] +
+                                                (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][4]) * 4);
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      gs.vw[i][s] = *reinterpret_cast<const uint4*>(
+          v.value_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][i]) * kRowBytes + 16 * quarter);
+}
+
+// Wave-level online-softmax state of the prefix path.  m is wave-uniform; l, mu0/mu1
+// (sum p*min per V half) are per lane over the lane's tokens; acc[j] holds channel
+// 16j + (lane&15) (replicated over the four lane quarters).
+struct WaveState {
+  float m, l, mu0, mu1;
+  float acc[8];
+};
+
+__device__ __forceinline__ v4i nib_lo(uint4 w) {
+  return v4i{static_cast<int>(w.x & 0x0F0F0F0Fu), static_cast<int>(w.y & 0x0F0F0F0Fu),
+             static_cast<int>(w.z & 0x0F0F0F0Fu), static_cast<int>(w.w & 0x0F0F0F0Fu)};
+}
+__device__ __forceinline__ v4i nib_hi(uint4 w) {
+  return v4i{static_cast<int>((w.x >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.y >> 4) & 0x0F0F0F0Fu),
+             static_cast<int>((w.z >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.w >> 4) & 0x0F0F0F0Fu)};
+}
+
+template <int NS, bool LOGITS>
+__device__ __forceinline__ void compute_group(const GroupSet<NS>& gs, WaveState& st, PrefixLds<NS>& L,
+                                              const DenseArgs& a, float* lgbuf) {
+  const int lane = threadIdx.x & 63, n = lane & 15, quarter = lane >> 4, q4 = lane & 3, digit = n & 3;
+  wave_lds_sync();  // the previous group's LDS reads are done before these writes
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) L.vt[s][i * 64 + lane] = gs.vw[i][s];
+
+  // ---- K side: y = q*scale per channel (lane: channels 2*lane, 2*lane+1), c_s = q.min
+  const float q0 = bf16lo_to_f32(gs.qw) * a.scaling, q1 = bf16hi_to_f32(gs.qw) * a.scaling;
+  float y0[NS], y1[NS], c[NS];
+  float ymax = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    y0[s] = q0 * gs.km[s].x;
+    y1[s] = q1 * gs.km[s].z;
+    ymax = fmaxf(ymax, fmaxf(fabsf(y0[s]), fabsf(y1[s])));
+    c[s] = fmaf(q0, gs.km[s].y, q1 * gs.km[s].w);
+  }
+  // streams 0/1 are present for every token: one reduction of their sum
+  c[0] = wave_sum(NS > 1 ? c[0] + c[1] : c[0]);
+  if (NS > 1) c[1] = 0.0f;
+#pragma unroll
+  for (int s = 2; s < NS; ++s) c[s] = wave_sum(c[s]);
+  ymax = wave_max(ymax);
+  const float yinv = ymax > 0.0f ? kFixScale * __builtin_amdgcn_rcpf(ymax) : 0.0f;
+  const float yunit = ymax * (1.0f / kFixScale);
+  // channel 2*lane = 32*quarter + 8*(n>>2) + 2*(n&3): parity 0, word (n>>2), byte (n&3)
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    L.y[s][q4][0][quarter][n >> 2] = quad_byte_transpose(fix_digits(y0[s], yinv), q4);
+    L.y[s][q4][1][quarter][n >> 2] = quad_byte_transpose(fix_digits(y1[s], yinv), q4);
+  }
+  wave_lds_sync();
+  v4i ae[NS], ao[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    ae[s] = *reinterpret_cast<const v4i*>(&L.y[s][digit][0][quarter][0]);
+    ao[s] = *reinterpret_cast<const v4i*>(&L.y[s][digit][1][quarter][0]);
+  }
+  float lg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v4i d = {0, 0, 0, 0};
+    float cadd = 0.0f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      if (s >= 2 && !hs.has[i][s]) continue;
-      const float we = p[i] * hs.vm[i][s].x;
-      const float wo = we * 0.0625f;
-      st.mu = fmaf(p[i], hs.vm[i][s].y, st.mu);
-      axpy8(hs.vw[i][s].x, we, wo, st.acc + 0);
-      axpy8(hs.vw[i][s].y, we, wo, st.acc + 8);
-      axpy8(hs.vw[i][s].z, we, wo, st.acc + 16);
-      axpy8(hs.vw[i][s].w, we, wo, st.acc + 24);
+      uint4 w = gs.kw[i][s];
+      bool ok = true;
+      if (s >= 2) {
+        ok = (gs.has >> (5 * (s - 2) + i)) & 1u;
+        if (!ok) w = make_uint4(0, 0, 0, 0);
+      }
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ae[s], nib_lo(w), d, 0, 0, 0);
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao[s], nib_hi(w), d, 0, 0, 0);
+      if (ok) cadd += c[s];
     }
+    lg[i] = fmaf(undigit(d), yunit, cadd);  // token 16i + n
+  }
+
+  // ---- softmax of the lane's own token (row = lane: tile `quarter`, position n)
+  const float lgo = quarter == 0 ? lg[0] : quarter == 1 ? lg[1] : quarter == 2 ? lg[2] : lg[3];
+  if (LOGITS) lgbuf[lane] = lgo;  // staged; written out in batches (see flush_logits)
+  const float gmax = wave_max(lgo);
+  if (gmax > st.m + kLazyRescale) {  // wave-uniform
+    const float alpha = st.m == -INFINITY ? 0.0f : fast_exp2((st.m - gmax) * kLog2e);
+    st.l *= alpha;
+    st.mu0 *= alpha;
+    st.mu1 *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st.acc[j] *= alpha;
+    st.m = gmax;
+  }
+  const float p = fast_exp2((lgo - st.m) * kLog2e);
+  st.l += p;
+  float z0[NS], z1[NS];
+  float zmax = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool ok = s < 2 || ((gs.has >> (5 * (s - 2) + 4)) & 1u);
+    z0[s] = ok ? p * gs.vm[s].x : 0.0f;
+    z1[s] = ok ? p * gs.vm[s].z : 0.0f;
+    if (ok) {
+      st.mu0 = fmaf(p, gs.vm[s].y, st.mu0);
+      st.mu1 = fmaf(p, gs.vm[s].w, st.mu1);
+    }
+    zmax = fmaxf(zmax, fmaxf(z0[s], z1[s]));
+  }
+  zmax = wave_max(zmax);
+  const float zinv = zmax > 0.0f ? kFixScale * __builtin_amdgcn_rcpf(zmax) : 0.0f;
+  const float zunit = zmax * (1.0f / kFixScale);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    L.z[s][0][q4][lane >> 2] = quad_byte_transpose(fix_digits(z0[s], zinv), q4);
+    L.z[s][1][q4][lane >> 2] = quad_byte_transpose(fix_digits(z1[s], zinv), q4);
+  }
+  wave_lds_sync();
+
+  // ---- P.V: channel tile j (16j .. 16j+15); lane (quarter, n) supplies row 16*quarter +
+  // sigma(n) so that the unpacked nibbles come out in token order 16*quarter + 0..15.
+  const int sig = (n & 8) | ((n & 1) << 2) | ((n >> 1) & 3);
+  v4i az[NS][2];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    az[s][0] = *reinterpret_cast<const v4i*>(&L.z[s][0][digit][4 * quarter]);
+    az[s][1] = *reinterpret_cast<const v4i*>(&L.z[s][1][digit][4 * quarter]);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    v4i d = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const char* base = reinterpret_cast<const char*>(&L.vt[s][0]) +
+                         (quarter * 64 + 16 * (j >> 1) + sig) * 16 + 8 * (j & 1);
+      const v2i t = __builtin_amdgcn_ds_read_tr4_b64_v2i32(
+          (lds_v2i*)((__attribute__((address_space(3))) char*)(base)));
+      const uint4 w = make_uint4(static_cast<uint32_t>(t[0]), static_cast<uint32_t>(t[0]) >> 4,
+                                 static_cast<uint32_t>(t[1]), static_cast<uint32_t>(t[1]) >> 4);
+      const v4i bop = {static_cast<int>(w.x & 0x0F0F0F0Fu), static_cast<int>(w.y & 0x0F0F0F0Fu),
+                       static_cast<int>(w.z & 0x0F0F0F0Fu), static_cast<int>(w.w & 0x0F0F0F0Fu)};
+      d = __builtin_amdgcn_mfma_i32_16x16x64_i8(az[s][j >> 2], bop, d, 0, 0, 0);
+    }
+    st.acc[j] = fmaf(undigit(d), zunit, st.acc[j]);
   }
 }
 
-template <int NS>
-__global__ __launch_bounds__(kThreads) void dense_reader_kernel(DenseArgs a) {
+__device__ __forceinline__ void reset_state(WaveState& st) {
+  st.m = -INFINITY;
+  st.l = st.mu0 = st.mu1 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.acc[j] = 0.0f;
+}
+
+// BF16 tail of the loop + the current token (virtual row tl) of row bh, by one wave:
+// lane = 4*row + quarter, 16 tokens per pass, 32 channels per lane; the 16 quad states
+// are merged through the wave's LDS (`comb`).
+template <bool LOGITS>
+__device__ void wave_tail(const DenseArgs& a, int bh, float (*comb)[kDim]) {
   const fl_cache_view& v = a.v;
-  const int split = blockIdx.x;
-  const int bh = blockIdx.y;
+  const int lane = threadIdx.x & 63, quarter = lane & 3, row = lane >> 2;
   const int b = bh / v.heads;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, quarter = lane & 3, row = lane >> 2;
-  // lengths come from device memory: clamp them to the buffers so a bad value cannot fault
-  const int Tp = min(v.packed_tokens[b], v.token_capacity) & ~(kGroup - 1);
-  const int tl = min(v.tail_tokens[b], v.tail_capacity);
-
-  __shared__ float qf[kDim];
-  __shared__ float qsh[kWaves][NS][kDim];
-  __shared__ float comb[kWaves][16][kDim];
-  __shared__ float lsh[kWaves * 16];
-  __shared__ float msh[kWaves];
-
-  if (tid < kDim) qf[tid] = bf16_to_f32(a.q[static_cast<int64_t>(bh) * kDim + tid]) * a.scaling;
-  __syncthreads();
-
+  const int Tp = row_groups(v, b) * kGroup;
+  const int tl = min(max(v.tail_tokens[b], 0), v.tail_capacity);
+  const uint16_t* tk = a.tail_k + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
+  const uint16_t* tv = a.tail_v + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
+  const uint16_t* ck = a.kc + static_cast<int64_t>(bh) * kDim;
+  const uint16_t* cv = a.vc + static_cast<int64_t>(bh) * kDim;
+  float* lrow = LOGITS ? a.logits + static_cast<int64_t>(bh) * a.logits_stride : nullptr;
+  float qr[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) qr[c] = bf16_to_f32(a.q[static_cast<int64_t>(bh) * kDim + 32 * quarter + c]) * a.scaling;
   QuadState st;
   st.m = -INFINITY;
   st.l = 0.0f;
   st.mu = 0.0f;
 #pragma unroll
   for (int c = 0; c < 32; ++c) st.acc[c] = 0.0f;
-
-  float* part = a.ws + (static_cast<int64_t>(bh) * (a.nsplit + 1) + split) * kPartial;
-  float* lrow = a.logits ? a.logits + static_cast<int64_t>(bh) * a.logits_stride : nullptr;
-
-  if (split < a.nsplit) {
-    const int G = Tp / kGroup;
-    const int g_begin = split * a.gps;
-    const int g_end = min(g_begin + a.gps, G);
-    const int gcap = v.token_capacity / kGroup;
-    // This wave's work: groups g_begin+wave, +kWaves, ... each as two half-groups of 32
-    // tokens (2 per lane).  Unit u = 2*k + h covers half h of the wave's k-th group.
-    const int my_groups = (g_end - g_begin - wave + kWaves - 1) / kWaves;
-    const int units = g_end - g_begin > wave ? 2 * my_groups : 0;
-    HalfSet<NS> set0, set1;
-    if (units > 0) load_half<NS>(set0, v, bh, b, g_begin + wave, 0, row, quarter, gcap);
-    for (int u = 0; u < units; u += 2) {
-      // ping-pong: the next unit's loads are in flight while this one computes
-      load_half<NS>(set1, v, bh, b, g_begin + wave + (u >> 1) * kWaves, 1, row, quarter, gcap);
-      dense_half<NS>(set0, st, a, qf, qsh[wave], b, g_begin + wave + (u >> 1) * kWaves, 0, row, quarter, lrow);
-      if (u + 2 < units) load_half<NS>(set0, v, bh, b, g_begin + wave + ((u >> 1) + 1) * kWaves, 0, row, quarter, gcap);
-      dense_half<NS>(set1, st, a, qf, qsh[wave], b, g_begin + wave + (u >> 1) * kWaves, 1, row, quarter, lrow);
-    }
-  } else {
-    // ---- BF16 tail of this loop, then the current token (virtual row tl)
-    const uint16_t* tk = a.tail_k + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
-    const uint16_t* tv = a.tail_v + static_cast<int64_t>(bh) * v.tail_capacity * kDim;
-    const uint16_t* ck = a.kc + static_cast<int64_t>(bh) * kDim;
-    const uint16_t* cv = a.vc + static_cast<int64_t>(bh) * kDim;
-    float qr[32];
-#pragma unroll
-    for (int c = 0; c < 32; ++c) qr[c] = qf[32 * quarter + c];
-    const int n = tl + 1;
-    for (int base = wave * 16; base < n; base += kWaves * 16) {
-      const int vt = base + row;
-      const bool valid = vt < n;
-      const uint16_t* kr = (vt < tl) ? tk + static_cast<int64_t>(vt) * kDim : ck;
-      const uint16_t* vr = (vt < tl) ? tv + static_cast<int64_t>(vt) * kDim : cv;
-      float d = 0.0f;
-      uint4 vwords[4];
-      if (valid) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const uint4 w = *reinterpret_cast<const uint4*>(kr + 32 * quarter + 8 * k);
-          d = fmaf(qr[8 * k + 0], bf16lo_to_f32(w.x), d);
-          d = fmaf(qr[8 * k + 1], bf16hi_to_f32(w.x), d);
-          d = fmaf(qr[8 * k + 2], bf16lo_to_f32(w.y), d);
-          d = fmaf(qr[8 * k + 3], bf16hi_to_f32(w.y), d);
-          d = fmaf(qr[8 * k + 4], bf16lo_to_f32(w.z), d);
-          d = fmaf(qr[8 * k + 5], bf16hi_to_f32(w.z), d);
-          d = fmaf(qr[8 * k + 6], bf16lo_to_f32(w.w), d);
-          d = fmaf(qr[8 * k + 7], bf16hi_to_f32(w.w), d);
-          vwords[k] = *reinterpret_cast<const uint4*>(vr + 32 * quarter + 8 * k);
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) vwords[k] = make_uint4(0, 0, 0, 0);
-      }
-      d = quad_sum(d);
-      float lg = valid ? d : -INFINITY;
-      if (lrow && quarter == 0 && valid) lrow[Tp + vt] = lg;
-      float p;
-      online_update(st, &lg, &p, 1);
+  const int n = tl + 1;
+  for (int base = 0; base < n; base += 16) {
+    const int vt = base + row;
+    const bool valid = vt < n;
+    const uint16_t* kr = (vt < tl) ? tk + static_cast<int64_t>(vt) * kDim : ck;
+    const uint16_t* vr = (vt < tl) ? tv + static_cast<int64_t>(vt) * kDim : cv;
+    float d = 0.0f;
+    uint4 vwords[4];
+    if (valid) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint32_t ws[4] = {vwords[k].x, vwords[k].y, vwords[k].z, vwords[k].w};
+        const uint4 w = *reinterpret_cast<const uint4*>(kr + 32 * quarter + 8 * k);
+        d = fmaf(qr[8 * k + 0], bf16lo_to_f32(w.x), d);
+        d = fmaf(qr[8 * k + 1], bf16hi_to_f32(w.x), d);
+        d = fmaf(qr[8 * k + 2], bf16lo_to_f32(w.y), d);
+        d = fmaf(qr[8 * k + 3], bf16hi_to_f32(w.y), d);
+        d = fmaf(qr[8 * k + 4], bf16lo_to_f32(w.z), d);
+        d = fmaf(qr[8 * k + 5], bf16hi_to_f32(w.z), d);
+        d = fmaf(qr[8 * k + 6], bf16lo_to_f32(w.w), d);
+        d = fmaf(qr[8 * k + 7], bf16hi_to_f32(w.w), d);
+        vwords[k] = *reinterpret_cast<const uint4*>(vr + 32 * quarter + 8 * k);
+      }
+    } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          st.acc[8 * k + 2 * e] = fmaf(p, bf16lo_to_f32(ws[e]), st.acc[8 * k + 2 * e]);
-          st.acc[8 * k + 2 * e + 1] = fmaf(p, bf16hi_to_f32(ws[e]), st.acc[8 * k + 2 * e + 1]);
-        }
+      for (int k = 0; k < 4; ++k) vwords[k] = make_uint4(0, 0, 0, 0);
+    }
+    d = quad_sum(d);
+    float lg = valid ? d : -INFINITY;
+    if (LOGITS && quarter == 0 && valid) lrow[Tp + vt] = lg;
+    float p;
+    online_update(st, &lg, &p, 1);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t ws[4] = {vwords[k].x, vwords[k].y, vwords[k].z, vwords[k].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        st.acc[8 * k + 2 * e] = fmaf(p, bf16lo_to_f32(ws[e]), st.acc[8 * k + 2 * e]);
+        st.acc[8 * k + 2 * e + 1] = fmaf(p, bf16hi_to_f32(ws[e]), st.acc[8 * k + 2 * e + 1]);
       }
     }
   }
-  write_partial(st, part, comb, lsh, msh);
+  const float M = wave_max(st.m);  // finite: the current token is always present
+  const float f = st.m == -INFINITY ? 0.0f : fast_exp2((st.m - M) * kLog2e);
+  wave_lds_sync();  // earlier LDS use of this wave is complete
+#pragma unroll
+  for (int c = 0; c < 32; ++c) comb[row][32 * quarter + c] = st.acc[c] * f;
+  const float L = wave_sum(quarter == 0 ? st.l * f : 0.0f);
+  wave_lds_sync();
+  float* part = a.ws + (static_cast<int64_t>(a.waves) + v.batch * v.heads + bh) * kPartial;  // tail slot
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    s0 += comb[r][2 * lane];
+    s1 += comb[r][2 * lane + 1];
+  }
+  part[2 + 2 * lane] = s0;
+  part[3 + 2 * lane] = s1;
+  if (lane == 0) {
+    part[0] = M;
+    part[1] = L;
+  }
 }
 
-int choose_gps(const fl_cache_view& v) {
+template <int NS>
+union WaveLds {
+  PrefixLds<NS> p;
+  float comb[16][kDim];
+};
+
+// Outputs of the prefix stream (logits of every group, one partial per row segment) are
+// staged in wave-private LDS and written after the wave's last load.  On gfx9-family
+// GPUs stores and loads share the in-order vmcnt counter, so a store issued mid-stream
+// holds up every later load wait until its write is acknowledged -- under a saturated
+// read stream that costs far more than the store's bytes.
+constexpr int kStageGroups = 64;  // logits of 64 groups (16 KB) per wave
+constexpr int kStageSegs = 4;     // partials of up to 4 row segments per wave
+
+// Row segments of the staged outputs live in wave-private LDS (a register array indexed
+// by a runtime count would be placed in scratch memory, whose accesses are vector memory
+// operations too).
+struct SegMeta {
+  int bh, gi0, first, count;
+};
+
+// Write the staged logits and partials of segments [0, n); the partial of segment n-1 is
+// skipped when it is still open.
+template <bool LOGITS>
+__device__ __forceinline__ void stage_flush(const DenseArgs& a, const SegMeta* seg, int n, const float* lgbuf,
+                                            const float (*pbuf)[kPartial], int w, bool last_open) {
+  const int lane = threadIdx.x & 63;
+  wave_lds_sync();
+  for (int k = 0; k < n; ++k) {
+    const SegMeta m = seg[k];
+    if (LOGITS) {
+      float* dst = a.logits + static_cast<int64_t>(m.bh) * a.logits_stride + static_cast<int64_t>(m.gi0) * kGroup;
+      const float* src = lgbuf + m.first * kGroup;
+      for (int e = lane; e < m.count * kGroup; e += kWave) dst[e] = src[e];
+    }
+    if (!(last_open && k == n - 1)) {
+      float* part = a.ws + partial_slot(w, m.bh) * kPartial;
+      for (int e = lane; e < kPartial; e += kWave) part[e] = pbuf[k][e];
+    }
+  }
+  wave_lds_sync();
+}
+
+// Stage the wave state of the current segment into pbuf[slot].
+__device__ __forceinline__ void stage_partial(const WaveState& st, float* part) {
+  const int lane = threadIdx.x & 63, n = lane & 15;
+  const float L = wave_sum(st.l), mu0 = wave_sum(st.mu0), mu1 = wave_sum(st.mu1);
+  if (lane < 16) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part[2 + 16 * j + n] = st.acc[j] + (j < 4 ? mu0 : mu1);
+  }
+  if (lane == 0) {
+    part[0] = st.m;
+    part[1] = L;
+  }
+}
+
+template <int NS, bool LOGITS>
+__global__ __launch_bounds__(kThreads) void dense_reader_kernel(DenseArgs a) {
+  __shared__ WaveLds<NS> sh[kWaves];
+  __shared__ float lgsh[LOGITS ? kWaves : 1][LOGITS ? kStageGroups * kGroup : 1];
+  __shared__ float psh[kWaves][kStageSegs][kPartial];
+  __shared__ SegMeta segsh[kWaves][kStageSegs];
+  const fl_cache_view& v = a.v;
+  const int wave = threadIdx.x >> 6;
+  const int w = blockIdx.x * kWaves + wave;
+  const int W = a.waves;
+  const int BH = v.batch * v.heads;
+
+  __shared__ int lens[kLenCache];
+  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kThreads) lens[i] = row_groups(v, i);
+  __syncthreads();
+  const RowLens rl{lens, min(v.batch, kLenCache)};
+  const int64_t U = total_units(v, rl);
+  const int64_t chunk = chunk_of(U, W);
+  const int64_t u0 = static_cast<int64_t>(w) * chunk;
+  const int64_t u1 = min(u0 + chunk, U);
+  if (u0 >= u1) return;
+
+  // Tails whose first unit lies in [u0, u1), then the count of prefix groups in range.
+  Cursor c = locate(v, rl, u0);
+  int my = 0;
+  {
+    Cursor t = c;
+    bool first = true;
+    while (t.b < v.batch && t.vs < u1) {
+      if (t.vs >= u0) wave_tail<LOGITS>(a, t.b * v.heads + t.h, sh[wave].comb);
+      const int64_t p0 = max(t.vs + kTailUnits, first ? u0 : t.vs), p1 = min(t.vs + kTailUnits + t.gb, u1);
+      if (p1 > p0) my += static_cast<int>(p1 - p0);
+      first = false;
+      next_row(t, v, rl);
+    }
+  }
+  if (my == 0) return;
+  // first prefix group in range
+  Cursor ld = c;
+  ld.gi = max(c.gi - kTailUnits, 0);
+  while (ld.gi >= ld.gb && ld.b < v.batch) next_row(ld, v, rl);
+  (void)BH;
+
+  WaveState st;
+  reset_state(st);
+  // Current segment in registers (wave-uniform); closed segments in LDS.
+  int nseg = 0, used = 0, cur_bh = -1, cur_gi0 = 0, cur_first = 0, cur_count = 0;
+  float* lgbuf = lgsh[LOGITS ? wave : 0];
+  float(*pbuf)[kPartial] = psh[wave];
+  SegMeta* seg = segsh[wave];
+  auto close_seg = [&]() {
+    stage_partial(st, pbuf[nseg - 1]);
+    if ((threadIdx.x & 63) == 0) seg[nseg - 1] = SegMeta{cur_bh, cur_gi0, cur_first, cur_count};
+  };
+  auto run = [&](const GroupSet<NS>& gs) {
+    if (gs.bh != cur_bh) {
+      if (nseg > 0) close_seg();
+      if (nseg == kStageSegs || (LOGITS && used == kStageGroups)) {  // rare: stage full
+        stage_flush<LOGITS>(a, seg, nseg, lgbuf, pbuf, w, false);
+        nseg = 0;
+        used = 0;
+      }
+      reset_state(st);
+      cur_bh = gs.bh;
+      cur_gi0 = gs.gi;
+      cur_first = used;
+      cur_count = 0;
+      ++nseg;
+    } else if (LOGITS && used == kStageGroups) {  // rare: logits stage full mid-segment
+      if ((threadIdx.x & 63) == 0) seg[nseg - 1] = SegMeta{cur_bh, cur_gi0, cur_first, cur_count};
+      stage_flush<LOGITS>(a, seg, nseg, lgbuf, pbuf, w, true);
+      nseg = 1;
+      used = 0;
+      cur_gi0 = gs.gi;
+      cur_first = 0;
+      cur_count = 0;
+    }
+    compute_group<NS, LOGITS>(gs, st, sh[wave].p, a, lgbuf + (LOGITS ? used * kGroup : 0));
+    ++used;
+    ++cur_count;
+  };
+  // Ping-pong: the next group's loads are in flight while a group computes.  The
+  // steady-state body issues its loads unconditionally: a load under a branch makes the
+  // waitcnt merge at the join wait for every outstanding load (vmcnt(0)).
+  GroupSet<NS> set0, set1;
+  load_group<NS>(set0, a, ld);
+  advance(ld, v, rl);
+  int k = 0;
+  for (; k + 2 < my; k += 2) {
+    load_group<NS>(set1, a, ld);
+    advance(ld, v, rl);
+    run(set0);
+    load_group<NS>(set0, a, ld);
+    advance(ld, v, rl);
+    run(set1);
+  }
+  if (my - k == 2) {
+    load_group<NS>(set1, a, ld);
+    run(set0);
+    run(set1);
+  } else {
+    run(set0);
+  }
+  close_seg();
+  stage_flush<LOGITS>(a, seg, nseg, lgbuf, pbuf, w, false);
+}
+
+// Combine row bh's partials: prefix slots [f+bh, l+bh] (see partial_slot) + its tail slot.
+__global__ __launch_bounds__(kDim) void dense_merge_kernel(const float* ws, int W, fl_cache_view v, float* out) {
+  __shared__ int lens[kLenCache];
+  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kDim) lens[i] = row_groups(v, i);
+  __syncthreads();
+  const RowLens rl{lens, min(v.batch, kLenCache)};
+  const int bh = blockIdx.x, c = threadIdx.x;
+  const int BH = v.batch * v.heads;
+  const int b = bh / v.heads, h = bh - (bh / v.heads) * v.heads;
+  int64_t vs = 0;
+  for (int bb = 0; bb < b; ++bb) vs += static_cast<int64_t>(v.heads) * (kTailUnits + rl(v, bb));
+  const int gb = rl(v, b);
+  vs += static_cast<int64_t>(h) * (kTailUnits + gb);
+  const int64_t U = total_units(v, rl);
+  int64_t f = 0, l = -1;
+  if (gb > 0) {
+    const int64_t chunk = chunk_of(U, W);
+    f = (vs + kTailUnits) / chunk;
+    l = (vs + kTailUnits + gb - 1) / chunk;
+  }
+  const float* tail = ws + (static_cast<int64_t>(W) + BH + bh) * kPartial;
+  float M = tail[0];
+  for (int64_t i = f; i <= l; ++i) M = fmaxf(M, ws[(i + bh) * kPartial]);
+  float L = 0.0f, acc = 0.0f;
+  {
+    const float e = tail[0] == -INFINITY ? 0.0f : fast_exp2((tail[0] - M) * kLog2e);
+    L = tail[1] * e;
+    acc = tail[2 + c] * e;
+  }
+  for (int64_t i = f; i <= l; ++i) {
+    const float* p = ws + (i + bh) * kPartial;
+    const float e = p[0] == -INFINITY ? 0.0f : fast_exp2((p[0] - M) * kLog2e);
+    L = fmaf(p[1], e, L);
+    acc = fmaf(p[2 + c], e, acc);
+  }
+  out[static_cast<int64_t>(bh) * kDim + c] = acc / L;
+}
+
+int cu_count() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> g(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Persistent grid: one 4-wave workgroup per CU (the reader holds 256 VGPRs per wave),
+// fewer when the problem is small.
+int persist_blocks(const fl_cache_view& v) {
   const int64_t rows = static_cast<int64_t>(v.batch) * v.heads;
-  const int64_t groups = v.max_packed_tokens / kGroup;
-  const int64_t target_blocks = 2048;
-  int64_t gps = (groups * rows + target_blocks - 1) / target_blocks;
-  gps = ((gps + kWaves - 1) / kWaves) * kWaves;  // whole iterations for every wave
-  if (gps < kWaves) gps = kWaves;
-  if (gps > 64) gps = 64;
-  return static_cast<int>(gps);
-}
-
-int nsplit_of(const fl_cache_view& v, int gps) {
-  const int groups = v.max_packed_tokens / kGroup;
-  return (groups + gps - 1) / gps;
+  const int64_t gmax = rows * (v.max_packed_tokens / kGroup);
+  const int64_t want = (gmax + rows * kTailUnits + kWaves - 1) / kWaves;
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cu_count(), want)));
 }
 
 }  // namespace
@@ -272,10 +711,9 @@ int nsplit_of(const fl_cache_view& v, int gps) {
 extern "C" size_t fl_decode_attn_dense_workspace(const fl_cache_view* view) {
   using namespace fl;
   if (!view) return 0;
-  const int gps = choose_gps(*view);
-  const int ns = nsplit_of(*view, gps);
-  const int rows = view->batch * view->heads;
-  return static_cast<size_t>(rows) * (ns + 1) * kPartial * sizeof(float);
+  const int64_t rows = static_cast<int64_t>(view->batch) * view->heads;
+  const int64_t waves = static_cast<int64_t>(persist_blocks(*view)) * kWaves;
+  return static_cast<size_t>(waves + 2 * rows) * kPartial * sizeof(float);
 }
 
 extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop, const uint16_t* q,
@@ -303,11 +741,9 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   FL_REQUIRE(logits == nullptr || logits_stride >= static_cast<int64_t>(v.max_packed_tokens) + v.max_tail_tokens + 1,
              "fl_decode_attn_dense: logits_stride smaller than the key count");
   FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense: workspace too small");
-  FL_REQUIRE(nsplit_of(v, choose_gps(v)) + 1 <= kMergeMaxParts, "fl_decode_attn_dense: context too long for one merge");
   FL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "fl_decode_attn_dense: workspace must be 16-byte aligned");
   DenseArgs a{};
   a.v = v;
-  a.loop = loop;
   a.q = q;
   a.kc = k_cur;
   a.vc = v_cur;
@@ -315,24 +751,26 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   a.logits = logits;
   a.logits_stride = logits_stride;
   a.ws = static_cast<float*>(workspace);
-  a.gps = choose_gps(v);
-  a.nsplit = nsplit_of(v, a.gps);
-  a.out = out;
   a.tail_k = v.tail_key[loop];
   a.tail_v = v.tail_value[loop];
-  const dim3 grid(a.nsplit + 1, v.batch * v.heads);
+  const int blocks = persist_blocks(v);
+  a.waves = blocks * kWaves;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (loop) {
-    case 0: hipLaunchKernelGGL(dense_reader_kernel<1>, grid, dim3(kThreads), 0, st, a); break;
-    case 1: hipLaunchKernelGGL(dense_reader_kernel<2>, grid, dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(dense_reader_kernel<3>, grid, dim3(kThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL(dense_reader_kernel<4>, grid, dim3(kThreads), 0, st, a); break;
+  const dim3 grid(blocks), block(kThreads);
+  const bool lg = logits != nullptr;
+  switch (loop * 2 + (lg ? 1 : 0)) {
+    case 0: hipLaunchKernelGGL((dense_reader_kernel<1, false>), grid, block, 0, st, a); break;
+    case 1: hipLaunchKernelGGL((dense_reader_kernel<1, true>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((dense_reader_kernel<2, false>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((dense_reader_kernel<2, true>), grid, block, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((dense_reader_kernel<3, false>), grid, block, 0, st, a); break;
+    case 5: hipLaunchKernelGGL((dense_reader_kernel<3, true>), grid, block, 0, st, a); break;
+    case 6: hipLaunchKernelGGL((dense_reader_kernel<4, false>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((dense_reader_kernel<4, true>), grid, block, 0, st, a); break;
   }
   FL_LAUNCH_CHECK("fl_decode_attn_dense(reader)");
-  hipLaunchKernelGGL(merge_partials_kernel, dim3(v.batch * v.heads), dim3(kDim), 0, st,
-                     static_cast<const float*>(a.ws), a.nsplit + 1, out, static_cast<int>(kMergeSoftmax),
-                     static_cast<const float*>(nullptr), static_cast<const float*>(nullptr),
-                     static_cast<const float*>(nullptr), static_cast<float*>(nullptr));
+  hipLaunchKernelGGL(dense_merge_kernel, dim3(v.batch * v.heads), dim3(kDim), 0, st,
+                     static_cast<const float*>(a.ws), a.waves, v, out);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(merge)");
   return FL_OK;
 }

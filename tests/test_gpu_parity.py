@@ -122,7 +122,9 @@ def test_dense_reader_all_loops(masked):
         want, want_lg = OA.dense_decode(q, K[loop], V[loop], np32(kc).reshape(6, 128),
                                         np32(vc).reshape(6, 128), SCALING)
         assert_close(np32(out).reshape(6, 128), want, what=f"loop {loop} output")
-        assert_close(np32(logits).reshape(6, -1), want_lg, max_abs=2e-2, mean_abs=5e-3, what=f"loop {loop} logits")
+        got_lg = np32(logits).reshape(6, -1)
+        assert got_lg.shape[1] >= want_lg.shape[1] and got_lg.shape[1] % 64 == 0  # padded, aligned row stride
+        assert_close(got_lg[:, : want_lg.shape[1]], want_lg, max_abs=2e-2, mean_abs=5e-3, what=f"loop {loop} logits")
 
 
 def test_topk_bit_exact_with_ties():
