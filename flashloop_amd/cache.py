@@ -61,8 +61,11 @@ class CrossLoopKVLayer:
         self.device = torch.device(device)
         rows = g.batch * g.heads
         dev = self.device
-        self.key_codes = [torch.zeros(rows, g.row_capacity[s], HEAD_DIM // 2, dtype=torch.uint8, device=dev) for s in range(4)]
-        self.value_codes = [torch.zeros(rows, g.row_capacity[s], HEAD_DIM // 2, dtype=torch.uint8, device=dev) for s in range(4)]
+        # one 128-byte line per token and stream: K codes in bytes 0..63, V codes in 64..127
+        self.codes = [torch.zeros(rows, g.row_capacity[s], 2 * (HEAD_DIM // 2), dtype=torch.uint8, device=dev)
+                      for s in range(4)]
+        self.key_codes = [c[..., : HEAD_DIM // 2] for c in self.codes]
+        self.value_codes = [c[..., HEAD_DIM // 2 :] for c in self.codes]
         self.key_meta = [torch.zeros(rows, g.token_capacity // GROUP, HEAD_DIM, 2, dtype=torch.float32, device=dev) for _ in range(4)]
         self.value_meta = [torch.zeros(rows, g.row_capacity[s], 2, 2, dtype=torch.float32, device=dev) for s in range(4)]
         self.rank = [torch.full((g.batch, g.token_capacity), -1, dtype=torch.int32, device=dev) for _ in range(2)]

@@ -223,22 +223,19 @@ __device__ __forceinline__ void load_group(GroupSet<NS>& gs, const DenseArgs& a,
   for (int s = 0; s < NS; ++s)
     gs.km[s] = *reinterpret_cast<const float4*>(v.key_meta[s] +
                                                 ((static_cast<int64_t>(bh) * gcap + gi) * kDim + 2 * lane) * 2);
+  // K and V halves of each 128-byte code line are requested back to back
 #pragma unroll
   for (int s = 0; s < NS; ++s)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      gs.kw[i][s] = *reinterpret_cast<const uint4*>(
-          v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][i]) * kRowBytes + 16 * quarter);
+    for (int i = 0; i < 4; ++i) {
+      const uint8_t* line = v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][i]) * kCodeStride;
+      gs.kw[i][s] = *reinterpret_cast<const uint4*>(line + 16 * quarter);
+      gs.vw[i][s] = *reinterpret_cast<const uint4*>(v.value_codes[s] - v.key_codes[s] + line + 16 * quarter);
+    }
 #pragma unroll
   for (int s = 0; s < NS; ++s)
     gs.vm[s] = *reinterpret_cast<const float4*>(v.value_meta[s] +
                                                 (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][4]) * 4);
-#pragma unroll
-  for (int s = 0; s < NS; ++s)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      gs.vw[i][s] = *reinterpret_cast<const uint4*>(
-          v.value_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][i]) * kRowBytes + 16 * quarter);
 }
 
 // Wave-level online-softmax state of the prefix path.  m is wave-uniform; l, mu0/mu1
@@ -645,41 +642,33 @@ __global__ __launch_bounds__(kThreads) void dense_reader_kernel(DenseArgs a) {
 }
 
 // Combine row bh's partials: prefix slots [f+bh, l+bh] (see partial_slot) + its tail slot.
-__global__ __launch_bounds__(kDim) void dense_merge_kernel(const float* ws, int W, fl_cache_view v, float* out) {
+__global__ __launch_bounds__(kMergeThreads) void dense_merge_kernel(const float* ws, int W, fl_cache_view v, float* out) {
   __shared__ int lens[kLenCache];
-  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kDim) lens[i] = row_groups(v, i);
+  __shared__ MergeLdsBuf S;
+  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kMergeThreads) lens[i] = row_groups(v, i);
   __syncthreads();
   const RowLens rl{lens, min(v.batch, kLenCache)};
-  const int bh = blockIdx.x, c = threadIdx.x;
+  const int bh = blockIdx.x;
   const int BH = v.batch * v.heads;
   const int b = bh / v.heads, h = bh - (bh / v.heads) * v.heads;
-  int64_t vs = 0;
-  for (int bb = 0; bb < b; ++bb) vs += static_cast<int64_t>(v.heads) * (kTailUnits + rl(v, bb));
+  int64_t vs = 0, U = 0;
+  for (int bb = 0; bb < v.batch; ++bb) {
+    const int64_t span = static_cast<int64_t>(v.heads) * (kTailUnits + rl(v, bb));
+    if (bb < b) vs += span;
+    U += span;
+  }
   const int gb = rl(v, b);
   vs += static_cast<int64_t>(h) * (kTailUnits + gb);
-  const int64_t U = total_units(v, rl);
   int64_t f = 0, l = -1;
   if (gb > 0) {
     const int64_t chunk = chunk_of(U, W);
     f = (vs + kTailUnits) / chunk;
     l = (vs + kTailUnits + gb - 1) / chunk;
   }
-  const float* tail = ws + (static_cast<int64_t>(W) + BH + bh) * kPartial;
-  float M = tail[0];
-  for (int64_t i = f; i <= l; ++i) M = fmaxf(M, ws[(i + bh) * kPartial]);
-  float L = 0.0f, acc = 0.0f;
-  {
-    const float e = tail[0] == -INFINITY ? 0.0f : fast_exp2((tail[0] - M) * kLog2e);
-    L = tail[1] * e;
-    acc = tail[2 + c] * e;
-  }
-  for (int64_t i = f; i <= l; ++i) {
-    const float* p = ws + (i + bh) * kPartial;
-    const float e = p[0] == -INFINITY ? 0.0f : fast_exp2((p[0] - M) * kLog2e);
-    L = fmaf(p[1], e, L);
-    acc = fmaf(p[2 + c], e, acc);
-  }
-  out[static_cast<int64_t>(bh) * kDim + c] = acc / L;
+  const MergeParts P{ws + (f + bh) * kPartial, static_cast<int>(l - f + 1),
+                     ws + (static_cast<int64_t>(W) + BH + bh) * kPartial};
+  const float r = merge_softmax(P, S);
+  if (threadIdx.x < kDim) out[static_cast<int64_t>(bh) * kDim + threadIdx.x] = r;
 }
 
 int cu_count() {
@@ -696,13 +685,47 @@ int cu_count() {
   return cached[dev];
 }
 
-// Persistent grid: one 4-wave workgroup per CU (the reader holds 256 VGPRs per wave),
-// fewer when the problem is small.
-int persist_blocks(const fl_cache_view& v) {
+// Resident workgroups per CU of a reader instantiation (cached per device).
+template <int NS, bool LOGITS>
+int occupancy() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+  std::lock_guard<std::mutex> g(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, dense_reader_kernel<NS, LOGITS>, kThreads, 0) != hipSuccess ||
+        n <= 0)
+      n = 1;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+int occupancy_of(int loop, bool logits) {
+  switch (loop * 2 + (logits ? 1 : 0)) {
+    case 0: return occupancy<1, false>();
+    case 1: return occupancy<1, true>();
+    case 2: return occupancy<2, false>();
+    case 3: return occupancy<2, true>();
+    case 4: return occupancy<3, false>();
+    case 5: return occupancy<3, true>();
+    case 6: return occupancy<4, false>();
+    default: return occupancy<4, true>();
+  }
+}
+
+constexpr int kMaxResident = 2;  // workgroups per CU any reader instantiation can hold
+
+// Persistent grid: every resident 4-wave workgroup slot of the GPU, fewer when the
+// problem is small.
+int persist_blocks(const fl_cache_view& v, int occ) {
   const int64_t rows = static_cast<int64_t>(v.batch) * v.heads;
   const int64_t gmax = rows * (v.max_packed_tokens / kGroup);
   const int64_t want = (gmax + rows * kTailUnits + kWaves - 1) / kWaves;
-  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cu_count(), want)));
+  const int64_t slots = static_cast<int64_t>(cu_count()) * std::min(std::max(occ, 1), kMaxResident);
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(slots, want)));
 }
 
 }  // namespace
@@ -712,7 +735,7 @@ extern "C" size_t fl_decode_attn_dense_workspace(const fl_cache_view* view) {
   using namespace fl;
   if (!view) return 0;
   const int64_t rows = static_cast<int64_t>(view->batch) * view->heads;
-  const int64_t waves = static_cast<int64_t>(persist_blocks(*view)) * kWaves;
+  const int64_t waves = static_cast<int64_t>(persist_blocks(*view, kMaxResident)) * kWaves;
   return static_cast<size_t>(waves + 2 * rows) * kPartial * sizeof(float);
 }
 
@@ -753,8 +776,10 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   a.ws = static_cast<float*>(workspace);
   a.tail_k = v.tail_key[loop];
   a.tail_v = v.tail_value[loop];
-  const int blocks = persist_blocks(v);
+  const int blocks = persist_blocks(v, occupancy_of(loop, logits != nullptr));
   a.waves = blocks * kWaves;
+  // a row has at most waves + 1 prefix partials (see partial_slot) plus its tail partial
+  FL_REQUIRE(a.waves + 2 <= kMergeMaxParts, "fl_decode_attn_dense: too many persistent waves for one merge");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(blocks), block(kThreads);
   const bool lg = logits != nullptr;
@@ -769,7 +794,7 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
     default: hipLaunchKernelGGL((dense_reader_kernel<4, true>), grid, block, 0, st, a); break;
   }
   FL_LAUNCH_CHECK("fl_decode_attn_dense(reader)");
-  hipLaunchKernelGGL(dense_merge_kernel, dim3(v.batch * v.heads), dim3(kDim), 0, st,
+  hipLaunchKernelGGL(dense_merge_kernel, dim3(v.batch * v.heads), dim3(kMergeThreads), 0, st,
                      static_cast<const float*>(a.ws), a.waves, v, out);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(merge)");
   return FL_OK;

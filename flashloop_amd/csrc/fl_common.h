@@ -13,7 +13,8 @@ namespace fl {
 
 constexpr int kDim = FL_HEAD_DIM;   // channels per head
 constexpr int kGroup = FL_GROUP;    // tokens per K group, channels per V group
-constexpr int kRowBytes = kDim / 2; // packed bytes per token row
+constexpr int kRowBytes = kDim / 2; // packed bytes per token row (K or V)
+constexpr int kCodeStride = FL_CODE_STRIDE;  // bytes between code rows: [K row | V row]
 constexpr int kWave = 64;
 
 // ---------------------------------------------------------------- host errors

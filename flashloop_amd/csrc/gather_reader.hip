@@ -74,8 +74,11 @@ __device__ __forceinline__ float dot_bf16_words(uint4 w, const float* q) {
   return d;
 }
 
+#ifndef FL_GATHER_MIN_BLOCKS
+#define FL_GATHER_MIN_BLOCKS 1
+#endif
 template <int NS, int MODE>
-__global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
+__global__ __launch_bounds__(kThreads, FL_GATHER_MIN_BLOCKS) void gather_reader_kernel(GatherArgs a) {
   const fl_cache_view& v = a.v;
   const int chunk = blockIdx.x;
   const int bh = blockIdx.y;
@@ -185,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
       kw[s] = make_uint4(0, 0, 0, 0);
       if (is_pre && rows[s] >= 0)
         kw[s] = *reinterpret_cast<const uint4*>(
-            v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s]) * kRowBytes + 16 * quarter);
+            v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s]) * kCodeStride + 16 * quarter);
     }
     if (nr > 0) load_meta(0);
   }
@@ -198,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
     vm[s] = make_float2(0.0f, 0.0f);
     if (is_pre && rows[s] >= 0) {
       const int64_t rowi = static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s];
-      vw[s] = *reinterpret_cast<const uint4*>(v.value_codes[s] + rowi * kRowBytes + 16 * quarter);
+      vw[s] = *reinterpret_cast<const uint4*>(v.value_codes[s] + rowi * kCodeStride + 16 * quarter);
       vm[s] = *reinterpret_cast<const float2*>(v.value_meta[s] + (rowi * 2 + (quarter >> 1)) * 2);
     }
   }
@@ -400,7 +403,7 @@ void launch_gather(GatherArgs& a, int rows, hipStream_t st) {
   }
   const int mode = MODE == kSelectedPV ? kMergeSum : (MODE == kSparseDelta ? kMergeMassDelta : kMergeMassDeltaFused);
   const float* ws2 = a.ws + static_cast<int64_t>(rows) * a.nchunk * kPartial;
-  hipLaunchKernelGGL(merge_partials_kernel, dim3(rows), dim3(kDim), 0, st, static_cast<const float*>(a.ws), a.nchunk,
+  hipLaunchKernelGGL(merge_partials_kernel, dim3(rows), dim3(kMergeThreads), 0, st, static_cast<const float*>(a.ws), a.nchunk,
                      a.out, mode, a.mass, a.src, ws2, a.src_out);
 }
 

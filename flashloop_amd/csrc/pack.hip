@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void pack_groups_kernel(PackArgs a) {
         const int row = row_active(a, r, b, src_row0 + i) ? dst_row(v, s, b, t) : -1;
         if (row >= 0) {
           const uint4 val = *reinterpret_cast<const uint4*>(&codes_lds[i][chunk * 16]);
-          *reinterpret_cast<uint4*>(v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + row) * kRowBytes +
+          *reinterpret_cast<uint4*>(v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + row) * kCodeStride +
                                     chunk * 16) = val;
         }
       }
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256) void pack_groups_kernel(PackArgs a) {
       const int row = act ? dst_row(v, s, b, t) : -1;
       if (row >= 0) {
         const int64_t rowi = static_cast<int64_t>(bh) * v.row_capacity[s] + row;
-        *reinterpret_cast<uint4*>(v.value_codes[s] + rowi * kRowBytes + 16 * quarter) =
+        *reinterpret_cast<uint4*>(v.value_codes[s] + rowi * kCodeStride + 16 * quarter) =
             make_uint4(words[0], words[1], words[2], words[3]);
         if ((quarter & 1) == 0) {
           *reinterpret_cast<float2*>(v.value_meta[s] + (rowi * 2 + half) * 2) = make_float2(q.scale, q.minimum);

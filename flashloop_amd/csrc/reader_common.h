@@ -110,66 +110,123 @@ __device__ void write_partial(QuadState& st, float* part, float (*comb)[16][kDim
 
 enum MergeMode { kMergeSoftmax = 0, kMergeMassDelta = 1, kMergeSum = 2 };
 
-// Combine a row's split partials (m, l, acc[128]); one workgroup of 128 threads per row.
+// Combine a row's partials (m, l, acc[128]).
 //   kMergeSoftmax:   out = sum_i e^{m_i-M} acc_i / sum_i e^{m_i-M} l_i
 //   kMergeMassDelta: out = mass * (softmax merge - src)
 //   kMergeSum:       out = sum_i acc_i
 //   kMergeMassDeltaFused: src = sum_i acc2_i (second partial set, written to src_out),
 //                    out = mass * (softmax merge - src)
-// The per-part weights e^{m_i-M} are formed once in LDS; the channel sums then issue
-// independent loads (unrolled) instead of a dependent chain per part.
+// Latency-bound, so every stage issues its loads at once: the per-part weights e^{m_i-M}
+// are formed by all threads into LDS, and each channel's sum is split over kMergeSplit
+// thread groups whose partial sums meet in LDS.
 constexpr int kMergeMassDeltaFused = 3;
 constexpr int kMergeMaxParts = 4096;
+constexpr int kMergeSplit = 4;
+constexpr int kMergeThreads = kDim * kMergeSplit;
 
-__global__ __launch_bounds__(kDim) void merge_partials_kernel(const float* ws, int nparts, float* out, int mode,
-                                                              const float* mass, const float* src,
-                                                              const float* ws2, float* src_out) {
-  __shared__ float f[kMergeMaxParts];
-  __shared__ float red[2];
-  const int bh = blockIdx.x, c = threadIdx.x;
-  const float* p = ws + static_cast<int64_t>(bh) * nparts * kPartial;
-  const int64_t o = static_cast<int64_t>(bh) * kDim + c;
-  const int n = min(nparts, kMergeMaxParts);
+// Part i of the row: `base + i*kPartial` for i < n_main, `extra` for i == n_main.
+struct MergeParts {
+  const float* base;
+  int n_main;
+  const float* extra;  // optional extra part (nullptr: none)
+  __device__ __forceinline__ int count() const { return n_main + (extra ? 1 : 0); }
+  __device__ __forceinline__ const float* part(int i) const {
+    return i < n_main ? base + static_cast<int64_t>(i) * kPartial : extra;
+  }
+};
+
+struct MergeLdsBuf {
+  float f[kMergeMaxParts];
+  float red[kMergeThreads / kWave];
+  float acc[kMergeSplit][kDim];
+};
+
+// Softmax merge of one row into out[c] (thread c < kDim writes); returns nothing.
+__device__ __forceinline__ float block_max_merge(float x, float* red) {
+  const int tid = threadIdx.x;
+  x = wave_max(x);
+  if ((tid & 63) == 0) red[tid >> 6] = x;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < kMergeThreads / kWave; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ float block_sum_merge(float x, float* red) {
+  const int tid = threadIdx.x;
+  x = wave_sum(x);
+  if ((tid & 63) == 0) red[tid >> 6] = x;
+  __syncthreads();
+  float r = 0.0f;
+  for (int w = 0; w < kMergeThreads / kWave; ++w) r += red[w];
+  __syncthreads();
+  return r;
+}
+
+// Channel sums sum_i w_i * part_i[2 + c] (w from LDS, or 1), split over kMergeSplit groups.
+template <bool WEIGHTED>
+__device__ __forceinline__ float merge_channel_sum(const MergeParts& P, const float* f, float (*acc)[kDim]) {
+  const int tid = threadIdx.x, c = tid & (kDim - 1), j = tid / kDim;
+  const int n = min(P.count(), kMergeMaxParts);
+  float s = 0.0f;
+#pragma unroll 16
+  for (int i = j; i < n; i += kMergeSplit) {
+    const float x = P.part(i)[2 + c];
+    s = WEIGHTED ? fmaf(x, f[i], s) : s + x;
+  }
+  acc[j][c] = s;
+  __syncthreads();
+  float r = 0.0f;
+  if (tid < kDim)
+#pragma unroll
+    for (int k = 0; k < kMergeSplit; ++k) r += acc[k][tid];
+  __syncthreads();
+  return r;  // valid for tid < kDim
+}
+
+__device__ __forceinline__ float merge_softmax(const MergeParts& P, MergeLdsBuf& S) {
+  const int tid = threadIdx.x;
+  const int n = min(P.count(), kMergeMaxParts);
+  float M = -INFINITY;
+  for (int i = tid; i < n; i += kMergeThreads) M = fmaxf(M, P.part(i)[0]);
+  M = block_max_merge(M, S.red);
+  float L = 0.0f;
+  for (int i = tid; i < n; i += kMergeThreads) {
+    const float* p = P.part(i);
+    const float m = p[0];
+    const float fi = (m == -INFINITY) ? 0.0f : fast_exp2((m - M) * kLog2e);
+    S.f[i] = fi;
+    L = fmaf(p[1], fi, L);
+  }
+  L = block_sum_merge(L, S.red);  // also orders the f[] writes before the reads below
+  const float acc = merge_channel_sum<true>(P, S.f, S.acc);
+  return acc / L;
+}
+
+__global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const float* ws, int nparts, float* out,
+                                                                       int mode, const float* mass, const float* src,
+                                                                       const float* ws2, float* src_out) {
+  __shared__ MergeLdsBuf S;
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int64_t o = static_cast<int64_t>(bh) * kDim + tid;
+  const MergeParts P{ws + static_cast<int64_t>(bh) * nparts * kPartial, nparts, nullptr};
   if (mode == kMergeSum) {
-    float acc = 0.0f;
-#pragma unroll 8
-    for (int i = 0; i < n; ++i) acc += p[i * kPartial + 2 + c];
-    out[o] = acc;
+    const float r = merge_channel_sum<false>(P, nullptr, S.acc);
+    if (tid < kDim) out[o] = r;
     return;
   }
-  float M = -INFINITY;
-  for (int i = c; i < n; i += kDim) M = fmaxf(M, p[i * kPartial]);
-  M = wave_max(M);
-  if ((c & 63) == 0) red[c >> 6] = M;
-  __syncthreads();
-  M = fmaxf(red[0], red[1]);
-  __syncthreads();
-  float L = 0.0f;
-  for (int i = c; i < n; i += kDim) {
-    const float m = p[i * kPartial];
-    const float fi = (m == -INFINITY) ? 0.0f : fast_exp2((m - M) * kLog2e);
-    f[i] = fi;
-    L = fmaf(p[i * kPartial + 1], fi, L);
+  float res = merge_softmax(P, S);
+  if (mode == kMergeMassDeltaFused) {
+    const MergeParts P2{ws2 + static_cast<int64_t>(bh) * nparts * kPartial, nparts, nullptr};
+    const float s = merge_channel_sum<false>(P2, nullptr, S.acc);
+    if (tid < kDim) {
+      src_out[o] = s;
+      res = mass[bh] * (res - s);
+    }
+  } else if (mode == kMergeMassDelta) {
+    if (tid < kDim) res = mass[bh] * (res - src[o]);
   }
-  L = wave_sum(L);
-  if ((c & 63) == 0) red[c >> 6] = L;
-  __syncthreads();
-  L = red[0] + red[1];
-  float acc = 0.0f;
-#pragma unroll 8
-  for (int i = 0; i < n; ++i) acc = fmaf(p[i * kPartial + 2 + c], f[i], acc);
-  float res = acc / L;
-  if (mode == kMergeMassDelta) {
-    res = mass[bh] * (res - src[o]);
-  } else if (mode == kMergeMassDeltaFused) {
-    const float* p2 = ws2 + static_cast<int64_t>(bh) * nparts * kPartial;
-    float s = 0.0f;
-#pragma unroll 8
-    for (int i = 0; i < n; ++i) s += p2[i * kPartial + 2 + c];
-    src_out[o] = s;
-    res = mass[bh] * (res - s);
-  }
-  out[o] = res;
+  if (tid < kDim) out[o] = res;
 }
 
 }  // namespace

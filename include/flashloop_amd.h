@@ -47,11 +47,14 @@ extern "C" {
  * and 3 store only the rows active in loops 3 and 4, at compact rows given by the
  * rank maps.  Code rows are token-major: byte j of a 64-byte row holds channel 2j in
  * its low nibble and channel 2j+1 in its high nibble (flashloop/packing.py:1-6, 49-54).
+ * The K and V rows of one token share one 128-byte line (FL_CODE_STRIDE): key_codes[s]
+ * points at byte 0 of row 0 and value_codes[s] at byte 64, consecutive rows are 128
+ * bytes apart, so a selected token costs one aligned line per stream.
  *
- *   key_codes[s]   u8  [B*H, row_capacity[s], 64]
+ *   key_codes[s]   u8  [B*H, row_capacity[s], 64]  row stride FL_CODE_STRIDE
  *   key_meta[s]    f32 [B*H, token_capacity/64, 128, 2]  (scale, min) per channel per
  *                      logical 64-token group (groups of streams 2/3 are logical too)
- *   value_codes[s] u8  [B*H, row_capacity[s], 64]
+ *   value_codes[s] u8  [B*H, row_capacity[s], 64]  row stride FL_CODE_STRIDE
  *   value_meta[s]  f32 [B*H, row_capacity[s], 2, 2]      (scale, min) per 64-channel half
  *   rank[0], rank[1] i32 [B, token_capacity]  compact row of stream 2 / 3, or -1
  *   tail_key[r], tail_value[r] bf16 [B*H, tail_capacity, 128]  loop r's BF16 tail
@@ -60,6 +63,8 @@ extern "C" {
  * Metadata is float32 so that the stored scale/min are bit-identical to the reference
  * codec (flashloop_torch/kv_quantization.py:395-414) and the residual chain stays exact.
  */
+#define FL_CODE_STRIDE 128 /* bytes between consecutive code rows of a stream */
+
 typedef struct fl_cache_view {
   int32_t batch;
   int32_t heads;
