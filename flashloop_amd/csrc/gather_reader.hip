@@ -12,22 +12,14 @@
 // (>= packed length) or a packed prefix row; prefix rows are rebuilt from streams
 // 0..loop, streams 2/3 through the rank maps.
 //
-// One workgroup owns kSlots consecutive selection slots, one 4-lane quad per slot
-// (lane = 4*quad_row + quarter, 32 channels per lane).  The K metadata of a 64-token
-// group is 1 KiB per stream and is shared by every selected token of that group (about
-// six at 10% selection), so it is read once per workgroup: slots are grouped into runs
-// of equal group (wave ballots), and each run's q*scale products and q.min constant are
-// staged in LDS before the quads take their dot products, as in the dense reader.
-// The workgroup's partial (max, sum, acc[128]) goes to the workspace; a small merge
-// kernel combines a row's partials.
 #include "reader_common.h"
+
+#include <mutex>
 
 namespace fl {
 namespace {
 using namespace reader;
 
-constexpr int kSlots = 64;  // selection slots per workgroup (one quad each)
-constexpr int kWin = 8;     // group runs whose K metadata is staged at once (a multiple of 4)
 
 enum GatherMode { kSparseDelta = 0, kSelectedPV = 1, kSparseDeltaFused = 2 };
 
@@ -46,13 +38,19 @@ struct GatherArgs {
   const uint16_t* tail_v1;
   int cap;
   float scaling;
-  float* ws;              // [B*H, nchunk, kPartial] (+ second set for the fused source aggregate)
-  int nchunk;
+  float* ws;              // partial slots [waves + B*H] (+ a second set for the fused source aggregate)
+  int waves;              // persistent waves in the grid
+  int tpr;                // tiles per row
   float* out;
   const float* mass;
   const float* src;       // source_output (kSparseDelta)
   float* src_out;         // source_output written (kSparseDeltaFused)
 };
+
+constexpr int kGatherSegs = 3;
+constexpr int kLenCacheG = 512;  // batches whose lengths a reader caches in LDS  // row segments a wave stages before writing partials
+
+__host__ __device__ __forceinline__ int64_t gather_slot(int w, int bh) { return static_cast<int64_t>(w) + bh; }
 
 __device__ __forceinline__ void axpy_bf16_words(uint4 w, float p, float* acc) {
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
@@ -74,293 +72,424 @@ __device__ __forceinline__ float dot_bf16_words(uint4 w, const float* q) {
   return d;
 }
 
-#ifndef FL_GATHER_MIN_BLOCKS
-#define FL_GATHER_MIN_BLOCKS 1
-#endif
-template <int NS, int MODE>
-__global__ __launch_bounds__(kThreads, FL_GATHER_MIN_BLOCKS) void gather_reader_kernel(GatherArgs a) {
-  const fl_cache_view& v = a.v;
-  const int chunk = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int b = bh / v.heads;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, quarter = lane & 3;
-  const int quad = tid >> 2;  // selection slot of this quad
-  // lengths come from device memory: clamp them to the buffers so a bad value cannot fault
-  const int Tp = min(v.packed_tokens[b], v.token_capacity) & ~(kGroup - 1);
-  const int tl = min(v.tail_tokens[b], v.tail_capacity);
-  const int cur = Tp + tl;
-  const int gcap = v.token_capacity / kGroup;
+// ---------------------------------------------------------------------------------
+// Persistent tile readers.  The selection of row bh is cut into tiles of T slots; wave
+// w of the grid owns tiles [w*chunk, min((w+1)*chunk, total)) of the row-major tile
+// sequence (chunk = ceil(total / waves)) and runs them one after another: a tile issues
+// all its loads at once (index, then rank rows / codes / metadata) and many resident
+// waves per CU overlap each other's load latencies.  Inside a tile LPT lanes own one
+// slot (lane = LPT*n + part, 128/LPT channels per lane, T = 64/LPT slots).
+//
+// K metadata is per 64-token group: the tile stages q*scale (per channel) and q.min
+// (per part) of W consecutive groups starting at its first prefix token's group in
+// wave-private LDS; tokens beyond the window are handled by further windows.
+// ---------------------------------------------------------------------------------
+template <int LPT>
+struct Lay {
+  static constexpr int kTok = kWave / LPT;       // slots per tile
+  static constexpr int kCh = kDim / LPT;         // channels per lane
+  static constexpr int kWords = kRowBytes / LPT / 4;  // code words per lane
+  static constexpr int kWin = LPT == 4 ? 4 : 2;  // K metadata window (groups)
+};
+
+template <int NS, int LPT>
+struct TileLds {
+  float qs[Lay<LPT>::kWin][NS][kDim];  // q*scale (odd channels pre-divided by 16)
+  float qm[Lay<LPT>::kWin][NS][LPT];   // q.min per part
+  float qf[kDim];                      // q*scaling of the current row
+};
+
+// Sum over the LPT lanes of a slot.
+template <int LPT>
+__device__ __forceinline__ float slot_sum(float x) {
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  if (LPT == 8) x += dpp<kDppHalfMirror>(x);
+  return x;
+}
+
+// Sum over the slots of a wave of values held per (slot, part): every lane gets the sum
+// over the lanes with its part.
+template <int LPT>
+__device__ __forceinline__ float slots_sum(float x) {
+  if (LPT == 4) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false));  // row_ror:4
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));  // row_ror:8
+  x += __shfl_xor(x, 16, kWave);
+  x += __shfl_xor(x, 32, kWave);
+  return x;
+}
+
+template <int LPT, int MODE>
+struct TileOut {
+  float m, l, mu, mu1;
+  float acc[Lay<LPT>::kCh];
+  float acc1[MODE == kSparseDeltaFused ? Lay<LPT>::kCh : 1];
+};
+
+template <int LPT, int MODE>
+__device__ __forceinline__ void tile_reset(TileOut<LPT, MODE>& o) {
+  o.m = (MODE == kSelectedPV) ? 0.0f : -INFINITY;
+  o.l = o.mu = o.mu1 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < Lay<LPT>::kCh; ++c) o.acc[c] = 0.0f;
+  if (MODE == kSparseDeltaFused) {
+#pragma unroll
+    for (int c = 0; c < Lay<LPT>::kCh; ++c) o.acc1[c] = 0.0f;
+  }
+}
+
+// Partial (m, l, acc[128]) of a wave segment -> staging LDS (second set: acc1 sums).
+template <int LPT, int MODE>
+__device__ __forceinline__ void tile_stage(const TileOut<LPT, MODE>& o, float* p, float* p1) {
+  constexpr int kCh = Lay<LPT>::kCh;
+  const int lane = threadIdx.x & 63, part = lane % LPT, n = lane / LPT;
+  const float l = wave_sum(part == 0 ? o.l : 0.0f);
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const float x = slots_sum<LPT>(o.acc[c] + o.mu);
+    if (n == 0) p[2 + kCh * part + c] = x;
+  }
+  if (lane == 0) {
+    p[0] = o.m;
+    p[1] = l;
+  }
+  if (MODE == kSparseDeltaFused) {
+#pragma unroll
+    for (int c = 0; c < kCh; ++c) {
+      const float x = slots_sum<LPT>(o.acc1[c] + o.mu1);
+      if (n == 0) p1[2 + kCh * part + c] = x;
+    }
+    if (lane == 0) {
+      p1[0] = 0.0f;
+      p1[1] = 0.0f;
+    }
+  }
+}
+
+template <int LPT>
+__device__ __forceinline__ void load_words(uint32_t* w, const uint8_t* src) {
+  if (LPT == 4) {
+    const uint4 x = *reinterpret_cast<const uint4*>(src);
+    w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+  } else {
+    const uint2 x = *reinterpret_cast<const uint2*>(src);
+    w[0] = x.x; w[1] = x.y;
+  }
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int NS, int MODE, int LPT>
+__global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
+  using Y = Lay<LPT>;
+  constexpr int kCh = Y::kCh, kWords = Y::kWords, kWin = Y::kWin;
   constexpr bool kSoftmax = MODE != kSelectedPV;
   constexpr bool kSource = MODE == kSparseDeltaFused;
+  constexpr int kSets = kSource ? 2 : 1;
+  __shared__ TileLds<NS, LPT> lds[kWaves];
+  __shared__ float stage[kWaves][kGatherSegs][kSets][kPartial];
+  __shared__ int seg_bh[kWaves][kGatherSegs];
+  const fl_cache_view& v = a.v;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, part = lane % LPT, n = lane / LPT;
+  const int half = part / (LPT / 2);
+  const int w = blockIdx.x * kWaves + wave;
+  TileLds<NS, LPT>& L = lds[wave];
+  const int rows = v.batch * v.heads;
+  const int tpr = a.cap / Y::kTok;  // tiles per row
+  const int64_t total = static_cast<int64_t>(rows) * tpr;
+  const int64_t chunk = (total + a.waves - 1) / a.waves;
+  const int64_t t0 = static_cast<int64_t>(w) * chunk;
+  const int64_t t1 = min(t0 + chunk, total);
+  const int gcap = v.token_capacity / kGroup;
 
-  __shared__ float qf[kDim];
-  __shared__ int tok[kSlots];
-  __shared__ int run_of[kSlots];
-  __shared__ int run_group[kSlots];
-  __shared__ int rows_sh[kSlots][NS];
-  __shared__ float pw[kSlots];
-  __shared__ float sw[kSlots];
-  // q*scale staging (logit phase) and the quad merge (end) never overlap: one LDS block
-  constexpr int kStage = kWin * NS * kDim + kWin * NS;
-  constexpr int kComb = kWaves * 16 * kDim;
-  __shared__ float lds_union[kStage > kComb ? kStage : kComb];
-  float(*qsh)[NS][kDim] = reinterpret_cast<float(*)[NS][kDim]>(lds_union);
-  float(*csh)[NS] = reinterpret_cast<float(*)[NS]>(lds_union + kWin * NS * kDim);
-  float(*comb)[16][kDim] = reinterpret_cast<float(*)[16][kDim]>(lds_union);
-  __shared__ float lsh[kWaves * 16];
-  __shared__ float msh[kWaves];
-  __shared__ int n_runs;
-
-  const int64_t sel0 = static_cast<int64_t>(bh) * a.cap + static_cast<int64_t>(chunk) * kSlots;
-  const int nslots = min(kSlots, a.cap - chunk * kSlots);
-
-  // ---- slot table: logical token, physical stream rows, runs of equal group (wave 0)
-  if (wave == 0) {
-    int t = -1;
-    if (lane < nslots) {  // index and flag loads issued together
-      const int ti = a.idx[sel0 + lane];
-      const bool ok = a.valid[sel0 + lane] != 0;
-      t = (ok && ti >= 0 && ti <= cur) ? ti : -1;  // out-of-range indices are dropped, never read
-    }
-    tok[lane] = t;
-    const bool pre = t >= 0 && t < Tp;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      int r = -1;
-      if (pre) {
-        if (s < 2) {
-          r = t;
-        } else {
-          r = v.rank[s - 2][static_cast<int64_t>(b) * v.token_capacity + t];
-          if (r >= v.row_capacity[s]) r = -1;
-        }
-      }
-      rows_sh[lane][s] = r;
-    }
-    const int g = pre ? t / kGroup : -1;
-    const int gprev = __shfl_up(g, 1, kWave);
-    const bool start = pre && (lane == 0 || gprev != g);
-    const uint64_t starts = __ballot(start);
-    const uint64_t le_mask = (lane == 63) ? ~0ull : ((2ull << lane) - 1);
-    const int run = pre ? __popcll(starts & le_mask) - 1 : -1;
-    run_of[lane] = run;
-    if (start) run_group[run] = g;
-    if (lane == 0) n_runs = __popcll(starts);
-    if (kSource) sw[lane] = (t >= 0) ? a.weights[sel0 + lane] : 0.0f;
-    if (MODE == kSelectedPV) pw[lane] = (t >= 0) ? a.weights[sel0 + lane] : 0.0f;
-  }
-  if (kSoftmax && tid < kDim) qf[tid] = bf16_to_f32(a.q[static_cast<int64_t>(bh) * kDim + tid]) * a.scaling;
-  lds_barrier();
-
-  const int t = tok[quad];
-  const int run = run_of[quad];
-  int rows[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) rows[s] = rows_sh[quad][s];
-
-  // Loads are issued in the order they are consumed -- K codes, the first window's K
-  // metadata, then the V rows -- because the memory counter retires in issue order:
-  // waiting for K must not also drain the V loads.
-  const bool is_pre = run >= 0;
-  const bool is_bf16 = t >= Tp;  // tail row or current token
-  constexpr int kRunsPerWave = kWin / kWaves;
-  const int nr = n_runs;
-  uint4 kw[NS];
-  float4 meta[kRunsPerWave][NS];
-  auto load_meta = [&](int w0) {
-    const int nw = min(kWin, nr - w0);
-#pragma unroll
-    for (int j = 0; j < kRunsPerWave; ++j) {
-      const int wr = wave + kWaves * j;
-      const int g = wr < nw ? run_group[w0 + wr] : 0;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        meta[j][s] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (wr < nw)
-          meta[j][s] = *reinterpret_cast<const float4*>(
-              v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + g) * kDim + 2 * lane) * 2);
+  auto write_stage = [&](int nseg) {
+    wave_sync_lds();
+    for (int k = 0; k < nseg; ++k) {
+      const int sb = seg_bh[wave][k];
+      for (int set = 0; set < kSets; ++set) {
+        float* dst = a.ws + (static_cast<int64_t>(set) * (a.waves + rows) + gather_slot(w, sb)) * kPartial;
+        for (int e = lane; e < kPartial; e += kWave) dst[e] = stage[wave][k][set][e];
       }
     }
   };
-  if (kSoftmax) {
+
+  // per-batch prefix length and current-token index, cached so the slot resolution of a
+  // tile needs no length load
+  __shared__ int len_tp[kLenCacheG], len_cur[kLenCacheG];
+  for (int i = threadIdx.x; i < min(v.batch, kLenCacheG); i += kThreads) {
+    // lengths come from device memory: clamp them to the buffers so a bad value cannot fault
+    const int tp = min(max(v.packed_tokens[i], 0), v.token_capacity) & ~(kGroup - 1);
+    len_tp[i] = tp;
+    len_cur[i] = tp + min(max(v.tail_tokens[i], 0), v.tail_capacity);
+  }
+  __syncthreads();
+
+  // Slot of this lane in a tile: token, stream rows, flags.  The index of tile j+1 is
+  // loaded and its rank rows requested while tile j's codes are in flight and computed.
+  struct Slot {
+    int bh, b, Tp, cur, t;
+    uint32_t has;
+    int row[NS];
+    float wt;
+  };
+  auto load_idx = [&](int64_t tile, int& ti, int& okv, float& wt) {
+    const int bh = static_cast<int>(tile / tpr);
+    const int64_t sel = static_cast<int64_t>(bh) * a.cap + (tile - static_cast<int64_t>(bh) * tpr) * Y::kTok + n;
+    ti = a.idx[sel];
+    okv = a.valid[sel];
+    wt = (MODE != kSparseDelta) ? a.weights[sel] : 0.0f;
+  };
+  auto resolve = [&](int64_t tile, int ti, int okv, float wt) {
+    Slot sl;
+    sl.bh = static_cast<int>(tile / tpr);
+    sl.b = sl.bh / v.heads;
+    sl.Tp = sl.b < kLenCacheG ? len_tp[sl.b] : (min(max(v.packed_tokens[sl.b], 0), v.token_capacity) & ~(kGroup - 1));
+    sl.cur = sl.b < kLenCacheG ? len_cur[sl.b] : sl.Tp + min(max(v.tail_tokens[sl.b], 0), v.tail_capacity);
+    sl.t = (okv != 0 && ti >= 0 && ti <= sl.cur) ? ti : -1;  // out-of-range indices are dropped, never read
+    sl.wt = wt;
+    const bool pre = sl.t >= 0 && sl.t < sl.Tp;
+    sl.has = 0;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      kw[s] = make_uint4(0, 0, 0, 0);
-      if (is_pre && rows[s] >= 0)
-        kw[s] = *reinterpret_cast<const uint4*>(
-            v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s]) * kCodeStride + 16 * quarter);
+      int r = pre ? sl.t : -1;
+      if (s >= 2 && pre) {
+        r = v.rank[s - 2][static_cast<int64_t>(sl.b) * v.token_capacity + sl.t];
+        if (r >= v.row_capacity[s]) r = -1;
+      }
+      if (r >= 0) sl.has |= 1u << s;
+      sl.row[s] = max(r, 0);
     }
-    if (nr > 0) load_meta(0);
-  }
-  uint4 vw[NS];
-  float2 vm[NS];
-  uint4 vbf[4];  // bf16 tail / current row (32 channels)
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    vw[s] = make_uint4(0, 0, 0, 0);
-    vm[s] = make_float2(0.0f, 0.0f);
-    if (is_pre && rows[s] >= 0) {
-      const int64_t rowi = static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s];
-      vw[s] = *reinterpret_cast<const uint4*>(v.value_codes[s] + rowi * kCodeStride + 16 * quarter);
-      vm[s] = *reinterpret_cast<const float2*>(v.value_meta[s] + (rowi * 2 + (quarter >> 1)) * 2);
-    }
-  }
-  const uint16_t* vrow1 = nullptr;  // loop-2 V row for the fused source aggregate
-  if (is_bf16) {
-    const uint16_t* vrow = (t == cur) ? a.vc + static_cast<int64_t>(bh) * kDim
-                                      : a.tail_v + (static_cast<int64_t>(bh) * v.tail_capacity + (t - Tp)) * kDim;
-    if (kSource)
-      vrow1 = (t == cur) ? a.vc1 + static_cast<int64_t>(bh) * kDim
-                         : a.tail_v1 + (static_cast<int64_t>(bh) * v.tail_capacity + (t - Tp)) * kDim;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) vbf[k] = *reinterpret_cast<const uint4*>(vrow + 32 * quarter + 8 * k);
-  }
+    return sl;
+  };
 
-  // ---- logits of the selected keys
-  float M = 0.0f;
-  if (kSoftmax) {
-    float d = 0.0f;
-    if (is_bf16) {
-      const uint16_t* krow =
-          (t == cur) ? a.kc + static_cast<int64_t>(bh) * kDim
-                     : a.tail_k + (static_cast<int64_t>(bh) * v.tail_capacity + (t - Tp)) * kDim;
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        d += dot_bf16_words(*reinterpret_cast<const uint4*>(krow + 32 * quarter + 8 * k), &qf[32 * quarter + 8 * k]);
+  TileOut<LPT, MODE> o;
+  tile_reset<LPT, MODE>(o);
+  int cur_bh = -1, nseg = 0;
+  if (t0 >= t1) {
+    write_stage(0);
+    return;
+  }
+  int ti_n, ok_n;
+  float wt_n;
+  load_idx(t0, ti_n, ok_n, wt_n);
+  Slot sl = resolve(t0, ti_n, ok_n, wt_n);
+
+  for (int64_t tile = t0; tile < t1; ++tile) {
+    const int64_t nxt = min(tile + 1, t1 - 1);  // the last tile re-reads its own index
+    load_idx(nxt, ti_n, ok_n, wt_n);
+    const int bh = sl.bh;
+    if (bh != cur_bh) {
+      if (cur_bh >= 0) {
+        if (nseg == kGatherSegs) {  // stage full: write it out (rare)
+          write_stage(nseg);
+          nseg = 0;
+        }
+        tile_stage<LPT, MODE>(o, stage[wave][nseg][0], kSource ? stage[wave][nseg][kSets - 1] : nullptr);
+        if (lane == 0) seg_bh[wave][nseg] = cur_bh;
+        ++nseg;
+        tile_reset<LPT, MODE>(o);
+      }
+      cur_bh = bh;
+      if (kSoftmax) {
+        wave_sync_lds();
+        const uint32_t qw = *reinterpret_cast<const uint32_t*>(a.q + static_cast<int64_t>(bh) * kDim + 2 * lane);
+        L.qf[2 * lane] = bf16lo_to_f32(qw) * a.scaling;
+        L.qf[2 * lane + 1] = bf16hi_to_f32(qw) * a.scaling;
+      }
     }
-    for (int w0 = 0; w0 < nr; w0 += kWin) {
-      // stage q*scale / q.min of runs [w0, w0+kWin): wave w owns runs w, w+kWaves, ...
-      // and all their streams (stream index known at compile time, so the metadata
-      // pointers stay in scalar registers)
-      if (w0 > 0) load_meta(w0);
-      const int nw = min(kWin, nr - w0);
-      const float q0 = qf[2 * lane], q1 = qf[2 * lane + 1];
+    const int t = sl.t, Tp = sl.Tp, cur = sl.cur;
+    const uint32_t has = sl.has;
+    const float wt = sl.wt;
+    const bool pre = t >= 0 && t < Tp;
+    const bool bf = t >= Tp;  // BF16 tail row or the current token
+    // codes and V metadata of every stream (rows clamped: absent rows read row 0, masked below)
+    uint32_t kw[NS][kWords], vw[NS][kWords];
+    float2 vm[NS];
 #pragma unroll
-      for (int j = 0; j < kRunsPerWave; ++j) {
-        const int wr = wave + kWaves * j;
-        if (wr < nw) {  // wave-uniform
+    for (int s = 0; s < NS; ++s) {
+      const uint8_t* line = v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + sl.row[s]) * kCodeStride;
+      if (kSoftmax) load_words<LPT>(kw[s], line + 4 * kWords * part);
+      load_words<LPT>(vw[s], v.value_codes[s] - v.key_codes[s] + line + 4 * kWords * part);
+      vm[s] = *reinterpret_cast<const float2*>(
+          v.value_meta[s] + ((static_cast<int64_t>(bh) * v.row_capacity[s] + sl.row[s]) * 2 + half) * 2);
+    }
+    // first K-metadata window: groups from the first prefix token's (slots are sorted)
+    const uint64_t pre_lanes = kSoftmax ? __ballot(pre) : 0;
+    int gwin = 0;
+    float4 km[kSoftmax ? kWin : 1][NS];
+    if (kSoftmax) {
+      const int first = pre_lanes ? __builtin_ctzll(pre_lanes) : 0;
+      const int tfirst = __shfl(t, first, kWave);
+      gwin = pre_lanes ? tfirst / kGroup : 0;
+#pragma unroll
+      for (int j = 0; j < kWin; ++j)
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          km[j][s] = *reinterpret_cast<const float4*>(
+              v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
+    }
+    // next tile's slot (rank rows fly while this tile computes)
+    sl = resolve(nxt, ti_n, ok_n, wt_n);
+
+    // ---- logits
+    float lg = 0.0f;
+    if (kSoftmax) {
+      const int gtok = pre ? t / kGroup : -1;
+      float d = 0.0f;
+      for (bool first_win = true;; first_win = false) {  // windows of kWin groups (wave-uniform)
+        if (!first_win) {
+#pragma unroll
+          for (int j = 0; j < kWin; ++j)
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+              km[j][s] = *reinterpret_cast<const float4*>(
+                  v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
+        }
+        const float q0 = L.qf[2 * lane], q1 = L.qf[2 * lane + 1];
+        wave_sync_lds();  // earlier reads of the window buffers are done
+#pragma unroll
+        for (int j = 0; j < kWin; ++j)
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
-            qsh[wr][s][2 * lane] = q0 * meta[j][s].x;
-            qsh[wr][s][2 * lane + 1] = q1 * meta[j][s].z * 0.0625f;  // high nibbles read as 16*code
-            const float c = wave_sum(fmaf(q0, meta[j][s].y, q1 * meta[j][s].w));
-            if (lane == 0) csh[wr][s] = c;
+            L.qs[j][s][2 * lane] = q0 * km[j][s].x;
+            L.qs[j][s][2 * lane + 1] = q1 * km[j][s].z * 0.0625f;  // high nibbles read as 16*code
+            // q.min over the channels of one part: fold the kCh/2 lanes holding them
+            float m = fmaf(q0, km[j][s].y, q1 * km[j][s].w);
+            m += dpp<kDppXor1>(m);
+            m += dpp<kDppXor2>(m);
+            m += dpp<kDppHalfMirror>(m);
+            if (LPT == 4) m += dpp<kDppMirror>(m);
+            if ((lane & (kCh / 2 - 1)) == 0) L.qm[j][s][lane / (kCh / 2)] = m;
+          }
+        wave_sync_lds();
+        const int js = gtok - gwin;
+        if (pre && js >= 0 && js < kWin) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            if (!((has >> s) & 1u)) continue;
+            const float* qq = &L.qs[js][s][kCh * part];
+            float e = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kWords; ++k) {
+              const float4 x = *reinterpret_cast<const float4*>(qq + 8 * k);
+              const float4 y = *reinterpret_cast<const float4*>(qq + 8 * k + 4);
+              const float qe[4] = {x.x, x.z, y.x, y.z}, qo[4] = {x.y, x.w, y.y, y.w};
+              e = dot8(kw[s][k], qe, qo, e);
+            }
+            d += e + L.qm[js][s][part];
           }
         }
+        // tokens past this window: another window
+        const uint64_t rest = __ballot(pre && js >= kWin);
+        if (!rest) break;
+        gwin = __shfl(t, __builtin_ctzll(rest), kWave) / kGroup;
       }
-      lds_barrier();
-      if (is_pre && run >= w0 && run < w0 + kWin) {
-        const int wr = run - w0;
+      // BF16 tail rows and the current token
+      if (__ballot(bf)) {
+        if (bf) {
+          const uint16_t* krow = (t == cur) ? a.kc + static_cast<int64_t>(bh) * kDim
+                                            : a.tail_k + (static_cast<int64_t>(bh) * v.tail_capacity + (t - Tp)) * kDim;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          if (rows[s] < 0) continue;
-          float qe[16], qo[16];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const float4 x = *reinterpret_cast<const float4*>(&qsh[wr][s][32 * quarter + 8 * k]);
-            const float4 y = *reinterpret_cast<const float4*>(&qsh[wr][s][32 * quarter + 8 * k + 4]);
-            qe[4 * k + 0] = x.x; qo[4 * k + 0] = x.y;
-            qe[4 * k + 1] = x.z; qo[4 * k + 1] = x.w;
-            qe[4 * k + 2] = y.x; qo[4 * k + 2] = y.y;
-            qe[4 * k + 3] = y.z; qo[4 * k + 3] = y.w;
-          }
-          float e = 0.0f;
-          e = dot8(kw[s].x, qe + 0, qo + 0, e);
-          e = dot8(kw[s].y, qe + 4, qo + 4, e);
-          e = dot8(kw[s].z, qe + 8, qo + 8, e);
-          e = dot8(kw[s].w, qe + 12, qo + 12, e);
-          d += e;
-          if (quarter == 0) d += csh[wr][s];
+          for (int k = 0; k < kCh / 8; ++k)
+            d += dot_bf16_words(*reinterpret_cast<const uint4*>(krow + kCh * part + 8 * k), &L.qf[kCh * part + 8 * k]);
         }
       }
-      lds_barrier();
-    }
-    d = quad_sum(d);
-    const float lg = (t >= 0) ? d : -INFINITY;
-    if (quarter == 0) pw[quad] = lg;
-    lds_barrier();
-    const float mt = wave_max(tid < kSlots ? pw[tid] : -INFINITY);
-    if (lane == 0) msh[wave] = mt;
-    lds_barrier();
-    M = fmaxf(fmaxf(msh[0], msh[1]), fmaxf(msh[2], msh[3]));
-    if (tid < kSlots) {
-      const float l = pw[tid];
-      pw[tid] = (l == -INFINITY) ? 0.0f : fast_exp2((l - M) * kLog2e);
-    }
-    lds_barrier();
-  }
-
-  // ---- P.V (and the fused loop-2 aggregate sum_S w V_1)
-  const float p = pw[quad];
-  const float w1 = kSource ? sw[quad] : 0.0f;
-  float acc[32], acc1[kSource ? 32 : 1];
-  float mu = 0.0f, mu1 = 0.0f;
+      d = slot_sum<LPT>(d);
+      lg = t >= 0 ? d : -INFINITY;
+      // online softmax over the wave's slots (m wave-uniform, rescaled lazily)
+      const float tmax = wave_max(lg);
+      if (tmax > o.m + 8.0f) {
+        const float alpha = o.m == -INFINITY ? 0.0f : fast_exp2((o.m - tmax) * kLog2e);
+        o.l *= alpha;
+        o.mu *= alpha;
 #pragma unroll
-  for (int c = 0; c < 32; ++c) acc[c] = 0.0f;
-  if (kSource) {
-#pragma unroll
-    for (int c = 0; c < 32; ++c) acc1[c] = 0.0f;
-  }
-  if (is_pre) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      if (rows[s] < 0) continue;
-      const float we = p * vm[s].x;
-      mu = fmaf(p, vm[s].y, mu);
-      axpy8(vw[s].x, we, we * 0.0625f, acc + 0);
-      axpy8(vw[s].y, we, we * 0.0625f, acc + 8);
-      axpy8(vw[s].z, we, we * 0.0625f, acc + 16);
-      axpy8(vw[s].w, we, we * 0.0625f, acc + 24);
-      if (kSource && s < 2) {
-        const float ws1 = w1 * vm[s].x;
-        mu1 = fmaf(w1, vm[s].y, mu1);
-        axpy8(vw[s].x, ws1, ws1 * 0.0625f, acc1 + 0);
-        axpy8(vw[s].y, ws1, ws1 * 0.0625f, acc1 + 8);
-        axpy8(vw[s].z, ws1, ws1 * 0.0625f, acc1 + 16);
-        axpy8(vw[s].w, ws1, ws1 * 0.0625f, acc1 + 24);
+        for (int c = 0; c < kCh; ++c) o.acc[c] *= alpha;
+        o.m = tmax;
       }
     }
-  } else if (is_bf16) {
+    const float p = kSoftmax ? (t >= 0 ? fast_exp2((lg - o.m) * kLog2e) : 0.0f) : (t >= 0 ? wt : 0.0f);
+    const float w1 = kSource ? (t >= 0 ? wt : 0.0f) : 0.0f;
+    o.l += p;
+
+    // ---- P.V (and the fused loop-2 aggregate sum_S w V_1)
+    if (pre) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) axpy_bf16_words(vbf[k], p, acc + 8 * k);
-    if (kSource) {
+      for (int s = 0; s < NS; ++s) {
+        if (!((has >> s) & 1u)) continue;
+        const float we = p * vm[s].x;
+        o.mu = fmaf(p, vm[s].y, o.mu);
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        axpy_bf16_words(*reinterpret_cast<const uint4*>(vrow1 + 32 * quarter + 8 * k), w1, acc1 + 8 * k);
+        for (int k = 0; k < kWords; ++k) axpy8(vw[s][k], we, we * 0.0625f, o.acc + 8 * k);
+        if (kSource && s < 2) {
+          const float ws1 = w1 * vm[s].x;
+          o.mu1 = fmaf(w1, vm[s].y, o.mu1);
+#pragma unroll
+          for (int k = 0; k < kWords; ++k) axpy8(vw[s][k], ws1, ws1 * 0.0625f, o.acc1 + 8 * k);
+        }
+      }
+    }
+    if (__ballot(bf)) {
+      if (bf) {
+        const uint16_t* vrow = (t == cur) ? a.vc + static_cast<int64_t>(bh) * kDim
+                                          : a.tail_v + (static_cast<int64_t>(bh) * v.tail_capacity + (t - Tp)) * kDim;
+#pragma unroll
+        for (int k = 0; k < kCh / 8; ++k)
+          axpy_bf16_words(*reinterpret_cast<const uint4*>(vrow + kCh * part + 8 * k), p, o.acc + 8 * k);
+        if (kSource) {
+          const uint16_t* vrow1 = (t == cur) ? a.vc1 + static_cast<int64_t>(bh) * kDim
+                                             : a.tail_v1 + (static_cast<int64_t>(bh) * v.tail_capacity + (t - Tp)) * kDim;
+#pragma unroll
+          for (int k = 0; k < kCh / 8; ++k)
+            axpy_bf16_words(*reinterpret_cast<const uint4*>(vrow1 + kCh * part + 8 * k), w1, o.acc1 + 8 * k);
+        }
+      }
     }
   }
-
-  // ---- workgroup partial(s), then the last workgroup of the row merges it
-  const int row = lane >> 2;
-  float* part = a.ws + (static_cast<int64_t>(bh) * a.nchunk + chunk) * kPartial;
-#pragma unroll
-  for (int c = 0; c < 32; ++c) comb[wave][row][32 * quarter + c] = acc[c] + mu;
-  if (quarter == 0) lsh[wave * 16 + row] = p;
-  lds_barrier();
-  if (tid < kDim) {
-    float s = 0.0f;
-    for (int w = 0; w < kWaves; ++w)
-      for (int r = 0; r < 16; ++r) s += comb[w][r][tid];
-    part[2 + tid] = s;
-  } else if (tid == kDim) {
-    float s = 0.0f;
-    for (int i = 0; i < kWaves * 16; ++i) s += lsh[i];
-    part[0] = (kSoftmax && s == 0.0f) ? -INFINITY : M;
-    part[1] = s;
+  if (cur_bh >= 0) {
+    if (nseg == kGatherSegs) {
+      write_stage(nseg);
+      nseg = 0;
+    }
+    tile_stage<LPT, MODE>(o, stage[wave][nseg][0], kSource ? stage[wave][nseg][kSets - 1] : nullptr);
+    if (lane == 0) seg_bh[wave][nseg] = cur_bh;
+    ++nseg;
   }
-  if (kSource) {
-    lds_barrier();
-    float* part1 = a.ws + (static_cast<int64_t>(gridDim.y) * a.nchunk + static_cast<int64_t>(bh) * a.nchunk + chunk) * kPartial;
-#pragma unroll
-    for (int c = 0; c < 32; ++c) comb[wave][row][32 * quarter + c] = acc1[c] + mu1;
-    lds_barrier();
+  write_stage(nseg);
+}
+
+// Merge of row bh: slots [f+bh, l+bh] of each partial set (see gather_slot).
+__global__ __launch_bounds__(kMergeThreads) void gather_merge_kernel(const float* ws, int waves, int tpr, int nrows,
+                                                                     float* out, int mode, const float* mass,
+                                                                     const float* src, float* src_out) {
+  __shared__ MergeLdsBuf S;
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int64_t total = static_cast<int64_t>(nrows) * tpr;
+  const int64_t chunk = (total + waves - 1) / waves;
+  const int64_t f = static_cast<int64_t>(bh) * tpr / chunk, l = (static_cast<int64_t>(bh + 1) * tpr - 1) / chunk;
+  const int64_t o = static_cast<int64_t>(bh) * kDim + tid;
+  const MergeParts P{ws + (f + bh) * kPartial, static_cast<int>(l - f + 1), nullptr};
+  if (mode == kMergeSum) {
+    const float r = merge_channel_sum<false>(P, nullptr, S.acc);
+    if (tid < kDim) out[o] = r;
+    return;
+  }
+  float res = merge_softmax(P, S);
+  if (mode == kMergeMassDeltaFused) {
+    const MergeParts P2{ws + (static_cast<int64_t>(waves) + nrows + f + bh) * kPartial, static_cast<int>(l - f + 1),
+                        nullptr};
+    const float s = merge_channel_sum<false>(P2, nullptr, S.acc);
     if (tid < kDim) {
-      float s = 0.0f;
-      for (int w = 0; w < kWaves; ++w)
-        for (int r = 0; r < 16; ++r) s += comb[w][r][tid];
-      part1[2 + tid] = s;
+      src_out[o] = s;
+      res = mass[bh] * (res - s);
     }
+  } else if (mode == kMergeMassDelta) {
+    if (tid < kDim) res = mass[bh] * (res - src[o]);
   }
+  if (tid < kDim) out[o] = res;
 }
 
 int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t* indices, const uint8_t* valid,
@@ -369,7 +498,7 @@ int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t
   const fl_cache_view& v = *view;
   FL_REQUIRE(loop >= 0 && loop <= 3, std::string(who) + ": loop must be in 0..3");
   FL_REQUIRE(indices && valid && workspace, std::string(who) + ": null indices/valid/workspace");
-  FL_REQUIRE(capacity > 0, std::string(who) + ": capacity must be positive");
+  FL_REQUIRE(capacity > 0 && capacity % 16 == 0, std::string(who) + ": capacity must be a positive multiple of 16");
   FL_REQUIRE(v.batch > 0 && v.heads > 0 && v.token_capacity % kGroup == 0, std::string(who) + ": bad view geometry");
   FL_REQUIRE(v.packed_tokens && v.tail_tokens, std::string(who) + ": null length arrays");
   FL_REQUIRE(v.tail_key[loop] && v.tail_value[loop], std::string(who) + ": null tail for this loop");
@@ -379,32 +508,83 @@ int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t
     if (s >= 2) FL_REQUIRE(v.rank[s - 2] != nullptr, std::string(who) + ": null rank map");
   }
   FL_REQUIRE(workspace_bytes >= need, std::string(who) + ": workspace too small");
-  FL_REQUIRE((capacity + kSlots - 1) / kSlots <= kMergeMaxParts, std::string(who) + ": capacity too large");
   FL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, std::string(who) + ": workspace must be 16-byte aligned");
   return FL_OK;
 }
 
-size_t gather_workspace(int rows, int capacity, int sets) {
-  const int nchunk = (capacity + kSlots - 1) / kSlots;
-  return static_cast<size_t>(rows) * nchunk * kPartial * sizeof(float) * sets;
+int gather_cu_count() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> g(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int NS, int MODE, int LPT>
+int gather_occupancy() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+  std::lock_guard<std::mutex> g(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gather_reader_kernel<NS, MODE, LPT>, kThreads, 0) != hipSuccess ||
+        n <= 0)
+      n = 1;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+constexpr int kGatherMaxResident = 4;  // workgroups per CU any reader instantiation holds
+
+// Persistent grid: every resident workgroup slot, fewer when the selection is small.
+int gather_blocks(int rows, int capacity, int occ) {
+  const int64_t tiles = static_cast<int64_t>(rows) * (capacity / 16);  // upper bound over tile sizes
+  const int64_t want = (tiles + kWaves - 1) / kWaves;
+  const int64_t slots = static_cast<int64_t>(gather_cu_count()) * std::min(std::max(occ, 1), kGatherMaxResident);
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(slots, want)));
+}
+
+size_t gather_workspace(int rows, int capacity) {
+  const int64_t waves = static_cast<int64_t>(gather_blocks(rows, capacity, kGatherMaxResident)) * kWaves;
+  return static_cast<size_t>(2 * (waves + rows)) * kPartial * sizeof(float);
+}
+
+#ifndef FL_GATHER_LPT
+#define FL_GATHER_LPT 8
+#endif
+constexpr int kLpt = FL_GATHER_LPT;  // lanes per selected slot
+
+template <int NS, int MODE>
+void launch_ns(GatherArgs& a, int rows, hipStream_t st) {
+  const int blocks = gather_blocks(rows, a.cap, gather_occupancy<NS, MODE, kLpt>());
+  a.waves = blocks * kWaves;
+  a.tpr = a.cap / Lay<kLpt>::kTok;
+  hipLaunchKernelGGL((gather_reader_kernel<NS, MODE, kLpt>), dim3(blocks), dim3(kThreads), 0, st, a);
 }
 
 template <int MODE>
 void launch_gather(GatherArgs& a, int rows, hipStream_t st) {
-  const dim3 grid(a.nchunk, rows);
   a.tail_k = a.v.tail_key[a.loop];
   a.tail_v = a.v.tail_value[a.loop];
   a.tail_v1 = a.v.tail_value[1];
   switch (a.loop) {
-    case 0: hipLaunchKernelGGL((gather_reader_kernel<1, MODE>), grid, dim3(kThreads), 0, st, a); break;
-    case 1: hipLaunchKernelGGL((gather_reader_kernel<2, MODE>), grid, dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((gather_reader_kernel<3, MODE>), grid, dim3(kThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL((gather_reader_kernel<4, MODE>), grid, dim3(kThreads), 0, st, a); break;
+    case 0: launch_ns<1, MODE>(a, rows, st); break;
+    case 1: launch_ns<2, MODE>(a, rows, st); break;
+    case 2: launch_ns<3, MODE>(a, rows, st); break;
+    default: launch_ns<4, MODE>(a, rows, st); break;
   }
   const int mode = MODE == kSelectedPV ? kMergeSum : (MODE == kSparseDelta ? kMergeMassDelta : kMergeMassDeltaFused);
-  const float* ws2 = a.ws + static_cast<int64_t>(rows) * a.nchunk * kPartial;
-  hipLaunchKernelGGL(merge_partials_kernel, dim3(rows), dim3(kMergeThreads), 0, st, static_cast<const float*>(a.ws), a.nchunk,
-                     a.out, mode, a.mass, a.src, ws2, a.src_out);
+  hipLaunchKernelGGL(gather_merge_kernel, dim3(rows), dim3(kMergeThreads), 0, st, static_cast<const float*>(a.ws),
+                     a.waves, a.tpr, rows, a.out, mode, a.mass, a.src, a.src_out);
 }
 
 }  // namespace
@@ -414,7 +594,7 @@ extern "C" size_t fl_decode_selected_workspace(const fl_cache_view* view, int32_
   using namespace fl;
   if (!view || capacity <= 0) return 0;
   // room for the fused variant's second partial set
-  return gather_workspace(view->batch * view->heads, capacity, 2);
+  return gather_workspace(view->batch * view->heads, capacity);
 }
 
 namespace {
@@ -444,7 +624,6 @@ extern "C" int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop
   a.weights = weights;
   a.cap = capacity;
   a.ws = gather_partials(workspace, rows);
-  a.nchunk = (capacity + kSlots - 1) / kSlots;
   a.out = out;
   launch_gather<kSelectedPV>(a, rows, static_cast<hipStream_t>(stream));
   FL_LAUNCH_CHECK("fl_decode_selected_pv");
@@ -475,7 +654,6 @@ extern "C" int32_t fl_decode_attn_sparse_delta(const fl_cache_view* view, int32_
   a.cap = capacity;
   a.scaling = scaling;
   a.ws = gather_partials(workspace, rows);
-  a.nchunk = (capacity + kSlots - 1) / kSlots;
   a.out = out;
   a.mass = mass;
   a.src = source_output;
@@ -515,7 +693,6 @@ extern "C" int32_t fl_decode_attn_sparse_delta_fused(const fl_cache_view* view, 
   a.cap = capacity;
   a.scaling = scaling;
   a.ws = gather_partials(workspace, rows);
-  a.nchunk = (capacity + kSlots - 1) / kSlots;
   a.out = out;
   a.mass = mass;
   a.src_out = source_output;
