@@ -47,7 +47,7 @@ struct DenseArgs {
 // row bh goes to slot w + bh: the slots of one row are contiguous and disjoint from every
 // other row's.
 // ---------------------------------------------------------------------------------
-constexpr int kTailUnits = 4;
+constexpr int kTailUnits = 3;  // measured best among 1..12 at cfg3 (contiguous-range wave partition)
 constexpr int kLenCache = 1024;  // batches whose group counts are cached in LDS
 
 __device__ __forceinline__ int row_groups(const fl_cache_view& v, int b) {
