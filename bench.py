@@ -35,6 +35,8 @@ MEASURED_TRAFFIC = {"cfg3": (1345.4 + 17.5) * 1e6}
 CONFIGS = {
     "cfg3": dict(batch=8, heads=16, tokens=32768, seed=3),
     "cfg1": dict(batch=1, heads=16, tokens=8192, seed=1),
+    # end-to-end random-init looped decoder, run through FlashLoopEngine
+    "cfg4": dict(prompt=8192, new_tokens=256, seed=4),
 }
 
 
@@ -45,6 +47,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=8, help="(b,h) rows of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--eager", action="store_true", help="cfg4: eager decode launches instead of HIP-graph replay")
     ap.add_argument("--fraction", type=float, default=0.10)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (a known-size kernel that "
@@ -80,12 +83,69 @@ def cpu_baseline(cfg, rows: int, fraction: float):
     return us_step, dt
 
 
+def bench_cfg4(args):
+    """Config 4: random-init Ouro-shaped model (24 layers, hidden 2048, 16 heads x 128,
+    SwiGLU 5632, vocab 49152, 4 loops), an 8192-token random prompt, greedy generation of
+    256 tokens through FlashLoopEngine (token retention 100/100/25/10%, 10% decode keys).
+    Reports prefill seconds and decode tokens/s; one JSON line."""
+    import torch
+
+    from flashloop_amd import FlashLoopEngine
+    from flashloop_amd.model import OuroConfig
+
+    cfg = CONFIGS["cfg4"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    print(f"[bench] cfg4: random-init model on {torch.cuda.get_device_name(0)}", file=sys.stderr, flush=True)
+    eng = FlashLoopEngine.from_random_init(OuroConfig(), seed=cfg["seed"], device=dev)
+    eng.use_graphs = not args.eager
+    g = torch.Generator().manual_seed(cfg["seed"])
+    ids = torch.randint(0, eng.model.config.vocab_size, (1, cfg["prompt"]), generator=g).to(dev)
+    new = cfg["new_tokens"] if args.steps == 50 else max(2, args.steps)
+    # warm-up on a short prompt (library loads, hipBLASLt heuristics)
+    eng.generate(ids[:, :640], max_new_tokens=4)
+    eng.reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = eng.prefill(ids, decode_capacity=new + 64)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    tok = torch.argmax(out.logits, dim=-1, keepdim=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(new - 1):
+        tok = torch.argmax(eng.decode(tok).logits, dim=-1, keepdim=True)
+    torch.cuda.synchronize()
+    decode_s = time.perf_counter() - t0
+    receipts = [dict(loop=r.loop, active_rows=r.active_rows) for r in eng.state.prefill_receipts]
+    line = {
+        "metric": "cfg4 end-to-end greedy decode tokens/s (random-init 24-layer looped decoder, prompt 8192)",
+        "value": round((new - 1) / decode_s, 2),
+        "unit": "tokens/s",
+        "ms_per_token": round(decode_s / (new - 1) * 1e3, 3),
+        "prefill_s": round(prefill_s, 4),
+        "new_tokens": new,
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "dtype": "bf16 weights / int4 KV",
+        "data": "synthetic (random weights, random token ids)",
+        "decode_graphs": eng.use_graphs,
+        "prefill_receipts": receipts,
+        "config": {"workload": "cfg4", "prompt": cfg["prompt"], "layers": eng.model.config.num_hidden_layers,
+                   "hidden": eng.model.config.hidden_size},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(the path shards by (batch, head) with no exchange; see DESIGN.md)"}))
         sys.exit(2)
+    if args.config == "cfg4":
+        bench_cfg4(args)
+        return
     import numpy as np
     import torch
 

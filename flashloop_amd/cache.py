@@ -76,6 +76,9 @@ class CrossLoopKVLayer:
         self.packed_tokens = torch.zeros(g.batch, dtype=torch.int32, device=dev)
         self.tail_tokens = torch.zeros(g.batch, dtype=torch.int32, device=dev)
         self.late_rows = torch.zeros(2, g.batch, dtype=torch.int32, device=dev)  # rows used in streams 2/3
+        self._row_index = None
+        self._batch_index = None
+        self._one_u8 = torch.ones((), dtype=torch.uint8, device=dev)
         # host mirrors (no device sync on the decode path)
         self.packed_host = [0] * g.batch
         self.tail_host = [0] * g.batch
@@ -228,10 +231,11 @@ class CrossLoopKVLayer:
 
     # ------------------------------------------------------------------ readers
     def logits_capacity(self) -> int:
-        """Row stride of the logits buffer: covers the longest prefix plus the longest tail
-        and the current token, rounded up to 64 floats so that every row starts on a
-        256-byte boundary (the reader writes logits in whole, aligned cache lines)."""
-        n = self.quantized_tokens + self.tail_tokens_max + 1
+        """Row stride of the logits buffer: covers the longest prefix plus a full tail and
+        the current token (constant between rollovers, so a captured decode step keeps
+        its buffers), rounded up to 64 floats so that every row starts on a 256-byte
+        boundary."""
+        n = self.quantized_tokens + self.geometry.tail_capacity + 1
         return (n + 63) // 64 * 64
 
     def dense_source_attention(self, loop: int, *, query, current_key, current_value, scaling: float,
@@ -300,30 +304,33 @@ class CrossLoopKVLayer:
     def append_decode_token(self, keys: Sequence[torch.Tensor], values: Sequence[torch.Tensor]) -> None:
         """``append_decode_token`` (flashloop/cache.py:1758-1776): write the step's four loop
         K/V rows (``[B,H,1,128]``) into the tails; roll a group out when a tail reaches 128."""
+        self.append_rows(keys, values)
+        self.commit_append()
+
+    def append_rows(self, keys: Sequence[torch.Tensor], values: Sequence[torch.Tensor]) -> None:
+        """Device half of an append: rows go to each sequence's device tail length, which is
+        then incremented -- no host index, so the step can be captured in a HIP graph.
+        ``commit_append`` must follow (host mirrors, rollover)."""
         if len(keys) != 4 or len(values) != 4:
             raise ValueError("exactly four loop K/V tensors are required")
-        b, h = self.batch, self.heads
-        cap = self.geometry.tail_capacity
-        if any(t >= cap for t in self.tail_host):
+        if any(t >= self.geometry.tail_capacity for t in self.tail_host):
             raise RuntimeError("tail is full; rollover did not run")
-        uniform = len(set(self.tail_host)) == 1
+        b, h = self.batch, self.heads
+        if self._row_index is None:
+            self._row_index = torch.arange(b * h, device=self.device)
+            self._batch_index = torch.arange(b, device=self.device)
+        pos = self.tail_tokens.long()
+        pos_rows = pos.repeat_interleave(h)
         for r in range(4):
-            k = keys[r].reshape(b * h, HEAD_DIM)
-            v = values[r].reshape(b * h, HEAD_DIM)
-            if uniform:
-                pos = self.tail_host[0]
-                self.tail_key[r][:, pos] = k
-                self.tail_value[r][:, pos] = v
-            else:
-                rows = torch.arange(b * h, device=self.device)
-                pos = torch.tensor(self.tail_host, device=self.device).repeat_interleave(h)
-                self.tail_key[r][rows, pos] = k
-                self.tail_value[r][rows, pos] = v
+            self.tail_key[r].index_put_((self._row_index, pos_rows), keys[r].reshape(b * h, HEAD_DIM))
+            self.tail_value[r].index_put_((self._row_index, pos_rows), values[r].reshape(b * h, HEAD_DIM))
         for s in range(2):
-            for bi in range(b):
-                self.tail_active[s][bi, self.tail_host[bi]] = 1
-        self.tail_host = [x + 1 for x in self.tail_host]
+            self.tail_active[s].index_put_((self._batch_index, pos), self._one_u8)
         self.tail_tokens += 1
+
+    def commit_append(self) -> None:
+        """Host half of an append: mirrors follow the device lengths; roll full tails."""
+        self.tail_host = [x + 1 for x in self.tail_host]
         if any(x >= self.residual_length + GROUP for x in self.tail_host):
             self._roll_groups()
 

@@ -184,7 +184,7 @@ __device__ __forceinline__ float merge_channel_sum(const MergeParts& P, const fl
   return r;  // valid for tid < kDim
 }
 
-__device__ __forceinline__ float merge_softmax(const MergeParts& P, MergeLdsBuf& S) {
+__device__ __forceinline__ float merge_softmax_general(const MergeParts& P, MergeLdsBuf& S) {
   const int tid = threadIdx.x;
   const int n = min(P.count(), kMergeMaxParts);
   float M = -INFINITY;
@@ -201,6 +201,50 @@ __device__ __forceinline__ float merge_softmax(const MergeParts& P, MergeLdsBuf&
   L = block_sum_merge(L, S.red);  // also orders the f[] writes before the reads below
   const float acc = merge_channel_sum<true>(P, S.f, S.acc);
   return acc / L;
+}
+
+// Softmax merge with every load in one round: thread (c, j) loads m, l and channel c of
+// parts j, j+kMergeSplit, ... (up to kMergeLocal each) before any arithmetic.
+constexpr int kMergeLocal = 8;
+
+__device__ __forceinline__ float merge_softmax(const MergeParts& P, MergeLdsBuf& S) {
+  const int n = min(P.count(), kMergeMaxParts);
+  if (n > kMergeSplit * kMergeLocal) return merge_softmax_general(P, S);
+  const int tid = threadIdx.x, c = tid & (kDim - 1), j = tid / kDim;
+  float mi[kMergeLocal], li[kMergeLocal], ai[kMergeLocal];
+#pragma unroll
+  for (int k = 0; k < kMergeLocal; ++k) {
+    const int i = j + kMergeSplit * k;
+    mi[k] = -INFINITY;
+    li[k] = 0.0f;
+    ai[k] = 0.0f;
+    if (i < n) {
+      const float* p = P.part(i);
+      mi[k] = p[0];
+      li[k] = p[1];
+      ai[k] = p[2 + c];
+    }
+  }
+  float M = mi[0];
+#pragma unroll
+  for (int k = 1; k < kMergeLocal; ++k) M = fmaxf(M, mi[k]);
+  M = block_max_merge(M, S.red);
+  float L = 0.0f, acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kMergeLocal; ++k) {
+    const float e = (mi[k] == -INFINITY) ? 0.0f : fast_exp2((mi[k] - M) * kLog2e);
+    L = fmaf(li[k], e, L);
+    acc = fmaf(ai[k], e, acc);
+  }
+  // L: every part counted once (by the c == 0 thread of its split group)
+  L = block_sum_merge(c == 0 ? L : 0.0f, S.red);
+  S.acc[j][c] = acc;
+  __syncthreads();
+  float r = 0.0f;
+  if (tid < kDim)
+#pragma unroll
+    for (int k = 0; k < kMergeSplit; ++k) r += S.acc[k][tid];
+  return r / L;  // valid for tid < kDim
 }
 
 __global__ __launch_bounds__(kMergeThreads) void merge_partials_kernel(const float* ws, int nparts, float* out,

@@ -90,7 +90,8 @@ def _budget(tokens: int, fraction: float) -> int:
 class FlashLoopEngine:
     """FlashLoop inference over an Ouro-shaped looped decoder, batch one."""
 
-    def __init__(self, model: OuroForCausalLM, *, config: FlashLoopConfig | None = None) -> None:
+    def __init__(self, model: OuroForCausalLM, *, config: FlashLoopConfig | None = None,
+                 use_graphs: bool = True) -> None:
         validate_ouro_model(model)
         self.model = model.eval()
         self.config = config or FlashLoopConfig()
@@ -98,6 +99,13 @@ class FlashLoopEngine:
         self.layers = model.model.layers
         self._state: EngineState | None = None
         self.observer: Callable[[str, dict], None] | None = None
+        # HIP-graph replay of decode steps (the per-layer launches of a step become one
+        # graph launch); off = eager launches
+        self.use_graphs = bool(use_graphs)
+        self._graph = None
+        self._graph_at = None
+        self._g_tok = self._g_pos = self._g_logits = None
+        self._g_counts: list[int] = []
 
     @classmethod
     def from_pretrained(cls, model_path: str, *, config: FlashLoopConfig | None = None,
@@ -118,6 +126,8 @@ class FlashLoopEngine:
 
     def reset(self) -> None:
         self._state = None
+        self._graph = None
+        self._graph_at = None
 
     # ------------------------------------------------------------------ prefill
     def _qkv(self, attn, x: torch.Tensor, rows: int):
@@ -227,23 +237,21 @@ class FlashLoopEngine:
         stage("physical_cache_finalized")
         receipts = (PrefillReceipt(1, t, t), PrefillReceipt(2, t, t), PrefillReceipt(3, t, n3), PrefillReceipt(4, t, n4))
         self._state = EngineState(cache, t, mask3, mask4, receipts)
+        self._graph = None  # a new cache: captured pointers are stale
         logits = self.model.lm_head(h4[:, -1]).float()
         stage("logits_ready")
         return PrefillOutput(logits=logits, state=self._state)
 
     # ------------------------------------------------------------------ decode
-    @torch.inference_mode()
-    def decode(self, token_ids: torch.Tensor) -> DecodeOutput:
-        """``FlashLoopEngine.decode`` (flashloop/engine.py:373-570)."""
+    def _decode_core(self, h: torch.Tensor, pos_t: torch.Tensor, pos: int) -> tuple[torch.Tensor, list[int]]:
+        """One decode step on the device: every layer and loop, then the cache appends
+        (device tail lengths, no host index).  ``pos_t`` holds the position on the device
+        (``pos`` only feeds host-side receipts).  Returns (logits, selected counts)."""
         state = self.state
-        if token_ids.shape != (1, 1):
-            raise ValueError("decode requires exactly one token at batch size one")
         cfg = self.config
         sparse = cfg.enable_sparse_decode
         fraction = cfg.effective_decode_key_fraction
-        h = self.backbone.embed_tokens(token_ids)
-        pos = state.next_position
-        cos, sin = self.backbone.rotary_emb(h, torch.tensor([[pos]], device=h.device))
+        cos, sin = self.backbone.rotary_emb(h, pos_t)
         nl = len(self.layers)
         cur_k = [[None] * 4 for _ in range(nl)]
         cur_v = [[None] * 4 for _ in range(nl)]
@@ -286,9 +294,17 @@ class FlashLoopEngine:
                 h = h + layer.post_attention_layernorm_2(layer.mlp(layer.post_attention_layernorm(h)))
             h = self.backbone.norm(h)
         for li in range(nl):
-            state.cache.layers[li].append_decode_token(cur_k[li], cur_v[li])
-        self._state = EngineState(state.cache, pos + 1, state.mask_loop3, state.mask_loop4, state.prefill_receipts)
-        logits = self.model.lm_head(h[:, -1]).float()
+            state.cache.layers[li].append_rows(cur_k[li], cur_v[li])
+        return self.model.lm_head(h[:, -1]).float(), counts
+
+    def _finish_step(self, logits: torch.Tensor, counts: list[int]) -> DecodeOutput:
+        state = self.state
+        for lc in state.cache.layers:
+            lc.commit_append()  # host mirrors; rolls a group out of full tails (outside any graph)
+        self._state = EngineState(state.cache, state.next_position + 1, state.mask_loop3, state.mask_loop4,
+                                  state.prefill_receipts)
+        nl = len(self.layers)
+        sparse = self.config.enable_sparse_decode
         receipt = DecodeReceipt(
             dense_attention_calls=(2 if sparse else 4) * nl,
             sparse_attention_calls=(2 if sparse else 0) * nl,
@@ -296,6 +312,60 @@ class FlashLoopEngine:
             selected_keys_per_layer=tuple(counts),
         )
         return DecodeOutput(logits=logits, state=self._state, receipt=receipt)
+
+    def _graph_key(self) -> tuple:
+        """Host-side values a captured step depends on: prefix lengths (rollover), the
+        selection capacity and the logits stride."""
+        lc = self.state.cache.layers[0]
+        cap = kernels.decode_capacity(lc.token_count + 1, self.config.effective_decode_key_fraction)
+        return (tuple(lc.packed_host), cap, lc.logits_capacity())
+
+    def _capture(self) -> None:
+        """Capture one decode step in a HIP graph.  A warm-up run on a side stream first sizes
+        every workspace and library handle; its append is then undone on the device (the
+        replay rewrites the same rows)."""
+        tok, pos_t = self._g_tok, self._g_pos
+        pos = self.state.next_position
+        side = torch.cuda.Stream()  # default priority
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._decode_core(self.backbone.embed_tokens(tok), pos_t, pos)
+            for lc in self.state.cache.layers:
+                lc.tail_tokens -= 1
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits, counts = self._decode_core(self.backbone.embed_tokens(tok), pos_t, pos)
+        self._graph, self._g_logits, self._g_counts = graph, logits, counts
+        self._graph_at = self._graph_key()
+
+    @torch.inference_mode()
+    def decode(self, token_ids: torch.Tensor) -> DecodeOutput:
+        """``FlashLoopEngine.decode`` (flashloop/engine.py:373-570).  With ``use_graphs`` the
+        step replays a captured HIP graph (recaptured when a rollover or the selection
+        capacity changes its shapes); the returned logits then live in the graph's output
+        buffer and are overwritten by the next step."""
+        state = self.state
+        if token_ids.shape != (1, 1):
+            raise ValueError("decode requires exactly one token at batch size one")
+        pos = state.next_position
+        if not self.use_graphs:
+            h = self.backbone.embed_tokens(token_ids)
+            pos_t = torch.tensor([[pos]], device=h.device)
+            logits, counts = self._decode_core(h, pos_t, pos)
+            return self._finish_step(logits, counts)
+        if self._g_tok is None:
+            self._g_tok = torch.zeros((1, 1), dtype=torch.long, device=token_ids.device)
+            self._g_pos = torch.zeros((1, 1), dtype=torch.long, device=token_ids.device)
+        self._g_tok.copy_(token_ids)
+        self._g_pos.fill_(pos)
+        if self._graph is None or self._graph_at != self._graph_key():
+            self._graph = None
+            self._capture()
+        self._graph.replay()
+        fraction = self.config.effective_decode_key_fraction
+        counts = [min(pos + 1, _budget(pos + 1, fraction))] * len(self._g_counts)
+        return self._finish_step(self._g_logits, counts)
 
     # ------------------------------------------------------------------ generate
     @torch.inference_mode()

@@ -103,3 +103,31 @@ def test_generate_crosses_rollover_and_hooks():
     assert joint["token_sparse_prefill"]["mask_nested"]
     assert joint["attention"]["target_replacements"] == 2 * TINY.num_hidden_layers * 69
     assert model.generate.__func__ is OuroForCausalLM.generate
+
+
+def test_graph_decode_matches_eager():
+    """Decode steps replayed from a captured HIP graph equal the eager launches bit for bit,
+    across two rollovers and a change of the selection capacity (which recapture), with
+    the eager rollover packing between replays."""
+    model = OuroForCausalLM.random_init(TINY, seed=7, device="cuda")
+    ids = _ids(700, seed=7)
+    eager = FlashLoopEngine(model, use_graphs=False)
+    graphed = FlashLoopEngine(model, use_graphs=True)
+    a = eager.prefill(ids[:, :600], decode_capacity=160).logits
+    b = graphed.prefill(ids[:, :600], decode_capacity=160).logits
+    assert torch.equal(a, b)
+    captures = 0
+    for i in range(600, 700):
+        tok = ids[:, i:i + 1]
+        da = eager.decode(tok)
+        before = graphed._graph
+        db = graphed.decode(tok)
+        captures += graphed._graph is not before
+        assert torch.equal(da.logits, db.logits), f"step {i}"
+        assert da.receipt == db.receipt
+    assert captures >= 3  # first capture, rollovers at 640 and 704-64, capacity step at 640
+    la, lb = eager.state.cache.layers[0], graphed.state.cache.layers[0]
+    assert la.packed_host == lb.packed_host and la.tail_host == lb.tail_host
+    for s in range(4):
+        assert torch.equal(la.codes[s], lb.codes[s])
+        assert torch.equal(la.tail_key[s], lb.tail_key[s])
