@@ -8,11 +8,12 @@
 //    (flashloop/selection.py:26-69).
 //
 // One workgroup of 1024 threads per row.  Scores are mapped to order-preserving
-// unsigned keys; four 8-bit histogram passes (LDS atomics) find the k-th largest key K*
-// and how many keys equal to K* to take.  A final pass walks the row in index order,
-// takes every key > K* and the first `need` keys == K* (ballot/popcount ranks), and
-// writes the selected indices in ascending order.  The row stays in L2 across passes
-// (131 KiB at 32K keys).
+// unsigned keys.  Decode rows of up to 35K keys are held in registers and selected in
+// one read (decode_topk_resident_kernel).  Longer rows and the prefill token selection
+// re-read the row (it stays in L2): four 8-bit histogram passes (LDS atomics) find the
+// k-th largest key K* and how many keys equal to K* to take, then a final pass walks the
+// row in index order, takes every key > K* and the first `need` keys == K*
+// (ballot/popcount ranks), and writes the selected indices in ascending order.
 #include "fl_common.h"
 
 namespace fl {
@@ -230,49 +231,60 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
   }
 }
 
-// LDS-resident variant for rows of at most kLdsKeys keys (gfx950: 160 KiB of LDS per
-// workgroup).  Passes over the row:
-//   1. load from HBM into LDS as order-preserving keys (all loads issued first);
+// Register-resident variant for rows of at most kResKeys keys and k <= kSelLds: thread t
+// holds keys t, t + 1024, t + 2048, ... in registers for the whole kernel, so no pass
+// after the load re-reads the row.  The passes are VALU-bound (one row per CU), so each
+// is kept to a few instructions per key:
+//   1. load as order-preserving keys (all loads issued first), row max and min;
 //   2. softmax normaliser and a histogram over kBins value-linear bins -- the bin is a
 //      non-decreasing function of the score, so the k-th largest key lies in the bin B*
 //      where the count from the top reaches k, and every key of a higher bin is larger;
-//   3. the keys of B* (a few dozen for smooth score distributions) are compacted into an
-//      LDS list and ranked there by (score desc, index asc), which fixes the k-th key
-//      (kth_key, kth_idx) -- a bin too crowded for the list falls back to an exact radix
-//      select restricted to B*;
-//   4. the selected keys (key > kth_key, or key == kth_key and index <= kth_idx) are
-//      written in index order: per (chunk, wave) ballot counts, one prefix scan, then
-//      each lane writes at its offset.
-constexpr int kLdsKeys = 35 * 1024;
-constexpr int kPer = kLdsKeys / kTopkThreads;
+//   3. per (chunk, wave) ballot counts of the keys above B*, and the keys of B* (a few
+//      dozen for smooth score distributions) compacted into an LDS list, ranked there by
+//      (score desc, index asc): that fixes the k-th key (kth_key, kth_idx) and adds the
+//      selected keys of B* to their (chunk, wave) counts -- a bin too crowded for the
+//      list falls back to an exact radix select restricted to B* and a counting pass;
+//   4. one prefix scan of the counts, then each lane stores its selected (index, key) at
+//      its offset in an LDS list, which is therefore in index order;
+//   5. the k list entries get their softmax weights and are written out coalesced.
+constexpr int kPer = 35;
+constexpr int kResKeys = kPer * kTopkThreads;
+constexpr int kSelLds = 8 * kTopkThreads;  // selected-list capacity of the resident kernel
+constexpr int kSelPer = kSelLds / kTopkThreads;
 constexpr int kSubHist = 4;
 constexpr int kBins = kSubHist * 256;  // value-linear bins of the boundary search (one per thread)
 constexpr int kCand = 512;             // boundary-bin list capacity
 static_assert(kBins == kTopkThreads, "one boundary bin per thread");
 
-// Non-decreasing in x; NaN products (inf - inf, 0 * inf) fall in bin 0, so the index is
-// always in range.
-__device__ __forceinline__ int value_bin(float x, float mn, float inv) {
-  const float b = (x - mn) * inv;
-  if (!(b > 0.0f)) return 0;
-  return b >= static_cast<float>(kBins - 1) ? kBins - 1 : static_cast<int>(b);
+// Non-decreasing in x (fma rounding is monotone for inv >= 0); NaN and negative products
+// fall in bin 0, so the index is always in range.  Every pass uses this one function.
+__device__ __forceinline__ int value_bin(float x, float inv, float off) {
+  const float b = fminf(fmaxf(fmaf(x, inv, off), 0.0f), static_cast<float>(kBins - 1));
+  return static_cast<int>(b);
 }
 
-struct LdsShared {
-  uint32_t keys[kLdsKeys];
+constexpr uint32_t kPadKey = 0x007FFFFFu;  // order_key(-inf)
+
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+struct ResShared {
   uint32_t hist[kSubHist][256];
   uint32_t cnt[kPer][kTopkWaves];  // per (chunk, wave) counts, then their exclusive prefix
   uint32_t cand_key[kCand];
   uint32_t cand_idx[kCand];
+  uint32_t cand_rank[kCand];
+  uint32_t sel_idx[kSelLds];
+  uint32_t sel_key[kSelLds];
   float red[kTopkWaves];
   uint32_t sel_digit;
   uint32_t bin_above;
   uint32_t ncand;
   uint32_t kth_key;
   uint32_t kth_idx;
+  uint32_t total;
 };
 
-__device__ float lds_block_max(float v, LdsShared& sh) {
+__device__ float res_block_max(float v, ResShared& sh) {
   v = wave_max(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
@@ -283,7 +295,7 @@ __device__ float lds_block_max(float v, LdsShared& sh) {
   return r;
 }
 
-__device__ float lds_block_sum(float v, LdsShared& sh) {
+__device__ float res_block_sum(float v, ResShared& sh) {
   v = wave_sum(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
@@ -296,8 +308,7 @@ __device__ float lds_block_sum(float v, LdsShared& sh) {
 
 // Exclusive prefix of sh.cnt in index order (chunk-major, wave-minor), done by wave 0;
 // returns the total.  Caller brackets it with barriers.
-__device__ uint32_t prefix_counts(LdsShared& sh) {
-  __shared__ uint32_t total;
+__device__ uint32_t prefix_counts(ResShared& sh) {
   if (threadIdx.x < kWave) {
     const int lane = threadIdx.x;
     constexpr int kN = kPer * kTopkWaves;
@@ -324,24 +335,24 @@ __device__ uint32_t prefix_counts(LdsShared& sh) {
       if (i < kN) c[i] = run;
       run += loc[e];
     }
-    if (lane == kWave - 1) total = incl;
+    if (lane == kWave - 1) sh.total = incl;
   }
   __syncthreads();
-  return total;
+  return sh.total;
 }
 
-__global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const float* scores, int64_t stride,
-                                                                       const int32_t* n_keys, int rows_per_count,
-                                                                       double fraction, int cap, int32_t* indices,
-                                                                       uint8_t* valid, float* mass, float* weights,
-                                                                       int32_t* counts) {
-  __shared__ LdsShared sh;
+__global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(const float* scores, int64_t stride,
+                                                                            const int32_t* n_keys, int rows_per_count,
+                                                                            double fraction, int cap, int32_t* indices,
+                                                                            uint8_t* valid, float* mass, float* weights,
+                                                                            int32_t* counts) {
+  __shared__ ResShared sh;
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const float* x = scores + static_cast<int64_t>(r) * stride;
   int n = min(n_keys[r / rows_per_count], static_cast<int>(min<int64_t>(stride, 0x7fffffff)));
-  n = min(n, kLdsKeys);
+  n = min(n, kResKeys);
   int32_t* oi = indices + static_cast<int64_t>(r) * cap;
   uint8_t* ov = valid + static_cast<int64_t>(r) * cap;
   float* ow = weights + static_cast<int64_t>(r) * cap;
@@ -352,6 +363,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
     if (k > n) k = n;
   }
   if (k > cap) k = cap;
+  if (k > kSelLds) k = kSelLds;  // the host routes rows that could exceed it elsewhere
   for (int j = k + tid; j < cap; j += kTopkThreads) {
     oi[j] = 0;
     ov[j] = 0;
@@ -365,7 +377,12 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
     return;
   }
 
-  // ---- 1. load
+  // ---- 1. load (slot j of thread t is index j * 1024 + t).  Slots past n hold kPadKey,
+  // the key of -inf, and real keys are clamped above it (a -inf score ranks as -FLT_MAX):
+  // padding then adds 0 to the normaliser, lands in bin 0 (whose count is corrected), is
+  // never a boundary candidate and never compares above the k-th key, so no later pass
+  // needs an index test.
+  uint32_t kr[kPer];
   float mx = -INFINITY, mn = INFINITY;
   {
     float xs[kPer];
@@ -376,9 +393,9 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
     }
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const int i = j * kTopkThreads + tid;
-      if (i < n) {
-        sh.keys[i] = order_key(xs[j]);
+      const bool in = j * kTopkThreads + tid < n;
+      kr[j] = in ? max(order_key(xs[j]), kPadKey + 1u) : kPadKey;
+      if (in) {
         mx = fmaxf(mx, xs[j]);
         mn = fminf(mn, xs[j]);
       }
@@ -386,28 +403,32 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
   }
   for (int i = tid; i < kBins; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
   if (tid == 0) sh.ncand = 0;
-  const float M = lds_block_max(mx, sh);
-  mn = -lds_block_max(-mn, sh);
-  // non-finite extremes collapse every key into bin 0 (the fallback then covers all)
+  const float M = res_block_max(mx, sh);
+  mn = -res_block_max(-mn, sh);
+  // bin(x) = clamp(x * inv - mn * inv); non-finite extremes collapse every key into bin 0
+  // (the crowded-bin fallback then covers all)
   const float inv = (isfinite(M) && isfinite(mn) && M > mn) ? static_cast<float>(kBins) / (M - mn) : 0.0f;
+  const float off = -mn * inv;
+  const float mlog = M * kLog2e;
 
   // ---- 2. normaliser and value histogram
   float z = 0.0f;
   uint32_t* lin = &sh.hist[0][0];  // one kBins-bin histogram (the sub-histograms are for the radix)
-  for (int i = tid; i < n; i += kTopkThreads) {
-    const float xi = key_value(sh.keys[i]);
-    z += fast_exp2((xi - M) * kLog2e);
-    atomicAdd(&lin[value_bin(xi, mn, inv)], 1u);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const float xi = key_value(kr[j]);
+    z += fast_exp2(fmaf(xi, kLog2e, -mlog));
+    atomicAdd(&lin[value_bin(xi, inv, off)], 1u);
   }
-  const float Z = lds_block_sum(z, sh);  // (its barriers also complete the histogram)
+  const float Z = res_block_sum(z, sh);  // (its barriers also complete the histogram)
   {
     const int bin = kBins - 1 - tid;  // descending scan: thread t owns bin kBins-1-t
-    const uint32_t h = lin[bin];
+    const uint32_t h = lin[bin] - (bin == 0 ? static_cast<uint32_t>(kResKeys - n) : 0u);
     uint32_t incl = h;
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const uint32_t o = __shfl_up(incl, off, kWave);
-      if (lane >= off) incl += o;
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t u = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += u;
     }
     if (lane == 63) sh.cnt[0][w] = incl;
     __syncthreads();
@@ -423,32 +444,63 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
   const int bstar = static_cast<int>(sh.sel_digit);
   const int need_b = k - static_cast<int>(sh.bin_above);  // >= 1 keys of B* are selected
 
-  // ---- 3. keys of the boundary bin -> (kth_key, kth_idx)
-  for (int i = tid; i < n; i += kTopkThreads) {
-    const uint32_t kk = sh.keys[i];
-    if (value_bin(key_value(kk), mn, inv) == bstar) {
-      const uint32_t slot = atomicAdd(&sh.ncand, 1u);
-      if (slot < kCand) {
-        sh.cand_key[slot] = kk;
+  // ---- 3. counts of the keys above B*; keys of B* -> LDS list (one LDS atomic per wave)
+  uint32_t cnt_lane = 0;  // lane j: this wave's count of chunk j
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * kTopkThreads + tid;
+    const int b = value_bin(key_value(kr[j]), inv, off);
+    const uint64_t bal_a = ballot64(b > bstar);
+    const bool in_b = b == bstar && kr[j] != kPadKey;
+    const uint64_t bal_b = ballot64(in_b);
+    cnt_lane = lane == j ? static_cast<uint32_t>(__popcll(bal_a)) : cnt_lane;
+    if (bal_b != 0ull) {
+      uint32_t base = 0;
+      if (lane == 0) base = atomicAdd(&sh.ncand, static_cast<uint32_t>(__popcll(bal_b)));
+      base = __shfl(base, 0, kWave);
+      const uint32_t slot = base + static_cast<uint32_t>(__popcll(bal_b & lt_mask));
+      if (in_b && slot < kCand) {
+        sh.cand_key[slot] = kr[j];
         sh.cand_idx[slot] = static_cast<uint32_t>(i);
       }
     }
   }
+  if (lane < kPer) sh.cnt[lane][w] = cnt_lane;
+  if (tid < kCand) sh.cand_rank[tid] = 0;
   __syncthreads();
   const int m = static_cast<int>(sh.ncand);
   if (m <= kCand) {
-    if (tid < m) {
-      const uint32_t mk = sh.cand_key[tid], mi = sh.cand_idx[tid];
-      int rank = 0;
-      for (int u = 0; u < m; ++u) {
+    // rank of each candidate = how many candidates precede it in (score desc, index asc)
+    // order.  The m x m comparisons are spread over all waves: wave w compares the 64
+    // candidates of block w % nb against slice w / nb of the list.
+    const int nb = (m + kWave - 1) / kWave;  // <= 8
+    const int slices = kTopkWaves / nb;
+    const int cb = w % nb, sl = w / nb;
+    if (sl < slices) {
+      const int c = cb * kWave + lane;
+      const int chunk = (m + slices - 1) / slices;
+      const int u0 = sl * chunk, u1 = min(m, u0 + chunk);
+      const uint32_t mk = c < m ? sh.cand_key[c] : 0u, mi = c < m ? sh.cand_idx[c] : 0u;
+      uint32_t rank = 0;
+#pragma unroll 4
+      for (int u = u0; u < u1; ++u) {
         const uint32_t uk = sh.cand_key[u], ui = sh.cand_idx[u];
-        rank += (uk > mk || (uk == mk && ui < mi)) ? 1 : 0;
+        rank += (uk > mk || (uk == mk && ui < mi)) ? 1u : 0u;
       }
+      if (c < m && rank) atomicAdd(&sh.cand_rank[c], rank);
+    }
+    __syncthreads();
+    // the need_b best are selected and join their (chunk, wave) count
+    if (tid < m) {
+      const uint32_t mi = sh.cand_idx[tid];
+      const int rank = static_cast<int>(sh.cand_rank[tid]);
+      if (rank < need_b) atomicAdd(&sh.cnt[mi / kTopkThreads][(mi % kTopkThreads) / kWave], 1u);
       if (rank == need_b - 1) {
-        sh.kth_key = mk;
+        sh.kth_key = sh.cand_key[tid];
         sh.kth_idx = mi;
       }
     }
+    __syncthreads();
   } else {
     // crowded bin (many equal or clustered scores): exact radix select within B*
     uint32_t prefix = 0, pmask = 0;
@@ -457,9 +509,10 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
     for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = tid; i < kSubHist * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
       __syncthreads();
-      for (int i = tid; i < n; i += kTopkThreads) {
-        const uint32_t kk = sh.keys[i];
-        if ((kk & pmask) == prefix && value_bin(key_value(kk), mn, inv) == bstar)
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const uint32_t kk = kr[j];
+        if (kk != kPadKey && (kk & pmask) == prefix && value_bin(key_value(kk), inv, off) == bstar)
           atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
       }
       __syncthreads();
@@ -476,9 +529,9 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
         }
         uint32_t incl = local;
 #pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-          const uint32_t o = __shfl_up(incl, off, kWave);
-          if (lane >= off) incl += o;
+        for (int o = 1; o < kWave; o <<= 1) {
+          const uint32_t u = __shfl_up(incl, o, kWave);
+          if (lane >= o) incl += u;
         }
         uint32_t above = incl - local;
 #pragma unroll
@@ -497,62 +550,81 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_lds_kernel(const flo
       __syncthreads();
     }
     // the `remaining`-th key equal to `prefix` in index order is the k-th key
-#pragma unroll 1
+#pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const int i = j * kTopkThreads + tid;
-      const bool eq = i < n && sh.keys[i] == prefix;
-      const uint64_t bal = __ballot(eq);
+      const bool eq = kr[j] == prefix;
+      const uint64_t bal = ballot64(eq);
       if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
     }
     __syncthreads();
     prefix_counts(sh);
-#pragma unroll 1
+#pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int i = j * kTopkThreads + tid;
-      const bool eq = i < n && sh.keys[i] == prefix;
-      const uint64_t bal = __ballot(eq);
+      const bool eq = kr[j] == prefix;
+      const uint64_t bal = ballot64(eq);
       const int rank = static_cast<int>(sh.cnt[j][w]) + __popcll(bal & lt_mask);
       if (eq && rank == remaining - 1) {
         sh.kth_key = prefix;
         sh.kth_idx = static_cast<uint32_t>(i);
       }
     }
+    __syncthreads();
+    const uint32_t kk0 = sh.kth_key, ki0 = sh.kth_idx;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * kTopkThreads + tid;
+      const uint32_t kk = kr[j];
+      const bool sel = kk > kk0 || (kk == kk0 && static_cast<uint32_t>(i) <= ki0);
+      const uint64_t bal = ballot64(sel);
+      if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const uint32_t kth_key = sh.kth_key;
   const uint32_t kth_idx = sh.kth_idx;
+  prefix_counts(sh);  // (its barrier also publishes the counts to every wave)
 
-  // ---- 4. selected keys in index order
-#pragma unroll 1
+  // ---- 4. selected (index, key) pairs into the LDS list, in index order
+  const uint32_t base_lane = lane < kPer ? sh.cnt[lane][w] : 0u;  // lane j: offset of chunk j
+#pragma unroll
   for (int j = 0; j < kPer; ++j) {
     const int i = j * kTopkThreads + tid;
-    const uint32_t kk = i < n ? sh.keys[i] : 0u;
-    const bool sel = i < n && (kk > kth_key || (kk == kth_key && static_cast<uint32_t>(i) <= kth_idx));
-    const uint64_t bal = __ballot(sel);
-    if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
-  }
-  __syncthreads();
-  prefix_counts(sh);
-  float msum = 0.0f;
-  const float invZ = 1.0f / Z;
-#pragma unroll 1
-  for (int j = 0; j < kPer; ++j) {
-    const int i = j * kTopkThreads + tid;
-    const uint32_t kk = i < n ? sh.keys[i] : 0u;
-    const bool sel = i < n && (kk > kth_key || (kk == kth_key && static_cast<uint32_t>(i) <= kth_idx));
-    const uint64_t bal = __ballot(sel);
-    const int pos = static_cast<int>(sh.cnt[j][w]) + __popcll(bal & lt_mask);
-    if (sel && pos < cap) {
-      const float wv = fast_exp2((key_value(kk) - M) * kLog2e) * invZ;
-      oi[pos] = i;
-      ov[pos] = 1;
-      ow[pos] = wv;
-      msum += wv;
+    const uint32_t kk = kr[j];
+    const bool sel = kk > kth_key || (kk == kth_key && static_cast<uint32_t>(i) <= kth_idx);
+    const uint64_t bal = ballot64(sel);
+    const int pos = static_cast<int>(__builtin_amdgcn_readlane(base_lane, j)) + __popcll(bal & lt_mask);
+    if (sel && pos < k) {
+      sh.sel_idx[pos] = static_cast<uint32_t>(i);
+      sh.sel_key[pos] = kk;
     }
   }
-  const float S = lds_block_sum(msum, sh);  // its barriers also order the weight writes
+  __syncthreads();
+
+  // ---- 5. weights of the k selected keys, coalesced output
+  const float invZ = 1.0f / Z;
+  float wv[kSelPer];
+  float msum = 0.0f;
+#pragma unroll
+  for (int e = 0; e < kSelPer; ++e) {
+    const int p = e * kTopkThreads + tid;
+    wv[e] = 0.0f;
+    if (p < k) {
+      wv[e] = fast_exp2(fmaf(key_value(sh.sel_key[p]), kLog2e, -mlog)) * invZ;
+      msum += wv[e];
+    }
+  }
+  const float S = res_block_sum(msum, sh);
   const float invS = 1.0f / S;
-  for (int j = tid; j < k; j += kTopkThreads) ow[j] *= invS;
+#pragma unroll
+  for (int e = 0; e < kSelPer; ++e) {
+    const int p = e * kTopkThreads + tid;
+    if (p < k) {
+      oi[p] = static_cast<int32_t>(sh.sel_idx[p]);
+      ov[p] = 1;
+      ow[p] = wv[e] * invS;
+    }
+  }
   if (tid == 0) {
     mass[r] = S;
     if (counts) counts[r] = k;
@@ -655,9 +727,9 @@ extern "C" int32_t fl_decode_topk(const float* scores, int64_t scores_stride, in
   if (rows == 0) return FL_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(rows), block(kTopkThreads);  // block: fallback kernel
-  // the stride bounds every row's key count: rows that fit in LDS take the one-read kernel
-  if (scores_stride <= kLdsKeys)
-    hipLaunchKernelGGL(decode_topk_lds_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+  // the stride bounds every row's key count: rows that fit in registers take the one-read kernel
+  if (scores_stride <= kResKeys && std::ceil(static_cast<double>(scores_stride) * fraction) <= kSelLds)
+    hipLaunchKernelGGL(decode_topk_resident_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
                        fraction, capacity, indices, valid, mass, weights, counts);
   else
     hipLaunchKernelGGL(decode_topk_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
