@@ -14,6 +14,8 @@ from .cache import (  # noqa: F401
     packed_prefix_tokens,
 )
 from .config import FlashLoopConfig  # noqa: F401
+from .batch_engine import FlashLoopBatchEngine
+from .batch_engine import FlashLoopBatchEngine  # noqa: F401
 from .engine import FlashLoopEngine  # noqa: F401
 from .hooks import flashloop  # noqa: F401
 
@@ -25,6 +27,7 @@ __all__ = [
     "decode_attention_step",
     "packed_prefix_tokens",
     "FlashLoopConfig",
+    "FlashLoopBatchEngine",
     "FlashLoopEngine",
     "flashloop",
 ]

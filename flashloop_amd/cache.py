@@ -381,6 +381,103 @@ class CrossLoopKVLayer:
         self.tail_tokens.copy_(torch.tensor(self.tail_host, dtype=torch.int32))
         self.late_rows.copy_(torch.tensor(self.late_rows_host, dtype=torch.int32))
 
+    # ------------------------------------------------------------------ serialization
+    # On-disk format (FORMAT_NAME, FORMAT_VERSION): one safetensors file whose tensors are
+    # the device buffers of the layer, byte for byte, under the names below (prefixed
+    # "layer{i}." inside a CrossLoopKVCache file), and whose string metadata holds a JSON
+    # header with the geometry and the host mirrors of the lengths:
+    #   codes.{s}        u8   [B*H, row_capacity[s], 128]  K codes (bytes 0..63) | V codes (64..127)
+    #   key_meta.{s}     f32  [B*H, token_capacity/64, 128, 2]  per-channel (scale, min) per group
+    #   value_meta.{s}   f32  [B*H, row_capacity[s], 2, 2]  per-token (scale, min) per 64 channels
+    #   rank.{j}         i32  [B, token_capacity]  logical token -> row of stream 2+j, or -1
+    #   tail_key.{r}     bf16 [B*H, tail_capacity, 128]  BF16 tail of loop r (tail_value likewise)
+    #   tail_active.{j}  u8   [B, tail_capacity]  loop-3/4 activity of the tail rows
+    #   packed_tokens / tail_tokens i32 [B], late_rows i32 [2, B]
+    FORMAT_NAME = "flashloop_amd.cross_loop_kv"
+    FORMAT_VERSION = 1
+
+    def _named_tensors(self) -> dict[str, torch.Tensor]:
+        named = {}
+        for s in range(4):
+            named[f"codes.{s}"] = self.codes[s]
+            named[f"key_meta.{s}"] = self.key_meta[s]
+            named[f"value_meta.{s}"] = self.value_meta[s]
+            named[f"tail_key.{s}"] = self.tail_key[s]
+            named[f"tail_value.{s}"] = self.tail_value[s]
+        for j in range(2):
+            named[f"rank.{j}"] = self.rank[j]
+            named[f"tail_active.{j}"] = self.tail_active[j]
+        named["packed_tokens"] = self.packed_tokens
+        named["tail_tokens"] = self.tail_tokens
+        named["late_rows"] = self.late_rows
+        return named
+
+    def _header(self) -> dict:
+        g = self.geometry
+        return {
+            "format": self.FORMAT_NAME, "version": self.FORMAT_VERSION,
+            "batch": g.batch, "heads": g.heads, "head_dim": HEAD_DIM, "group_size": GROUP,
+            "residual_length": self.residual_length, "token_capacity": g.token_capacity,
+            "tail_capacity": g.tail_capacity, "row_capacity": list(g.row_capacity),
+            "packed_tokens": list(self.packed_host), "tail_tokens": list(self.tail_host),
+            "late_rows": [list(x) for x in self.late_rows_host],
+        }
+
+    def state_dict(self) -> tuple[dict[str, torch.Tensor], dict]:
+        """(tensors, header) of the layer in the on-disk format above (tensors are the
+        live buffers, not copies)."""
+        return self._named_tensors(), self._header()
+
+    @classmethod
+    def from_state_dict(cls, tensors: dict[str, torch.Tensor], header: dict, device) -> "CrossLoopKVLayer":
+        """Rebuild a layer from ``state_dict`` output; every shape and dtype is checked
+        against the header before anything is copied."""
+        if header.get("format") != cls.FORMAT_NAME:
+            raise ValueError(f"not a {cls.FORMAT_NAME} payload")
+        if int(header.get("version", -1)) != cls.FORMAT_VERSION:
+            raise ValueError(f"unsupported format version {header.get('version')} (expected {cls.FORMAT_VERSION})")
+        if int(header["head_dim"]) != HEAD_DIM or int(header["group_size"]) != GROUP \
+                or int(header["residual_length"]) != cls.residual_length:
+            raise ValueError("head_dim / group_size / residual_length differ from this build's")
+        g = LayerGeometry(int(header["batch"]), int(header["heads"]), int(header["token_capacity"]),
+                          int(header["tail_capacity"]), tuple(int(x) for x in header["row_capacity"]))
+        layer = cls(g, device)
+        want = layer._named_tensors()
+        if set(tensors) != set(want):
+            raise ValueError(f"tensor set differs: missing {sorted(set(want) - set(tensors))}, "
+                             f"unexpected {sorted(set(tensors) - set(want))}")
+        for name, dst in want.items():
+            src = tensors[name]
+            if tuple(src.shape) != tuple(dst.shape) or src.dtype != dst.dtype:
+                raise ValueError(f"{name}: {tuple(src.shape)} {src.dtype} != {tuple(dst.shape)} {dst.dtype}")
+            dst.copy_(src)
+        layer.packed_host = [int(x) for x in header["packed_tokens"]]
+        layer.tail_host = [int(x) for x in header["tail_tokens"]]
+        layer.late_rows_host = [[int(x) for x in r] for r in header["late_rows"]]
+        if len(layer.packed_host) != g.batch or len(layer.tail_host) != g.batch:
+            raise ValueError("length mirrors do not match the batch")
+        if [int(x) for x in layer.packed_tokens.tolist()] != layer.packed_host \
+                or [int(x) for x in layer.tail_tokens.tolist()] != layer.tail_host:
+            raise ValueError("device lengths disagree with the header")
+        return layer
+
+    def save(self, path: str) -> None:
+        from safetensors.torch import save_file
+        import json
+
+        tensors, header = self.state_dict()
+        save_file({k: v.contiguous() for k, v in tensors.items()}, path, metadata={"header": json.dumps(header)})
+
+    @classmethod
+    def load(cls, path: str, device="cuda") -> "CrossLoopKVLayer":
+        from safetensors import safe_open
+        import json
+
+        with safe_open(path, framework="pt", device="cpu") as f:
+            header = json.loads(f.metadata()["header"])
+            tensors = {k: f.get_tensor(k) for k in f.keys()}
+        return cls.from_state_dict(tensors, header, device)
+
     # ------------------------------------------------------------------ accounting
     @property
     def storage_bytes(self) -> int:
@@ -437,6 +534,40 @@ class CrossLoopKVCache:
     @property
     def storage_bytes(self) -> int:
         return sum(layer.storage_bytes for layer in self.layers if layer is not None)
+
+    def save(self, path: str) -> None:
+        """Every installed layer in one safetensors file (tensor names ``layer{i}.<name>``,
+        per-layer headers in the metadata); see CrossLoopKVLayer for the tensor layout."""
+        from safetensors.torch import save_file
+        import json
+
+        tensors, headers = {}, {}
+        for i, layer in enumerate(self.layers):
+            if layer is None:
+                continue
+            named, header = layer.state_dict()
+            tensors.update({f"layer{i}.{k}": v.contiguous() for k, v in named.items()})
+            headers[str(i)] = header
+        meta = {"format": CrossLoopKVLayer.FORMAT_NAME, "version": CrossLoopKVLayer.FORMAT_VERSION,
+                "num_layers": len(self.layers), "layers": headers}
+        save_file(tensors, path, metadata={"header": json.dumps(meta)})
+
+    @classmethod
+    def load(cls, path: str, device="cuda") -> "CrossLoopKVCache":
+        from safetensors import safe_open
+        import json
+
+        with safe_open(path, framework="pt", device="cpu") as f:
+            meta = json.loads(f.metadata()["header"])
+            if meta.get("format") != CrossLoopKVLayer.FORMAT_NAME:
+                raise ValueError(f"not a {CrossLoopKVLayer.FORMAT_NAME} file")
+            cache = cls(num_layers=int(meta["num_layers"]))
+            for key, header in meta["layers"].items():
+                i = int(key)
+                pre = f"layer{i}."
+                tensors = {k[len(pre):]: f.get_tensor(k) for k in f.keys() if k.startswith(pre)}
+                cache.set_layer(i, CrossLoopKVLayer.from_state_dict(tensors, header, device))
+        return cache
 
 
 @dataclass

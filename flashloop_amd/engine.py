@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
-from typing import Callable
+from typing import Callable, Sequence
 
 import torch
 import torch.nn.functional as F
@@ -80,11 +80,85 @@ class _LayerSource:
     selected_weights: torch.Tensor
     current_value: torch.Tensor
     selected_output: torch.Tensor | None = None
-    count: int = 0
 
 
 def _budget(tokens: int, fraction: float) -> int:
     return max(1, math.ceil(tokens * fraction))
+
+
+@dataclass
+class _PrefillLoops:
+    keys: list  # [loop][layer] -> [1, H, T, 128] bf16
+    values: list
+    mask3: torch.Tensor  # [1, T] bool
+    mask4: torch.Tensor
+    receipts: tuple
+    logits: torch.Tensor  # [1, vocab] f32
+
+
+class DecodeRunner:
+    """Runs decode steps of one engine's ``_decode_core``: eagerly, or replayed from a HIP
+    graph captured per regime (the per-layer launches of a step become one graph
+    launch).  The regime is every host value the captured step depends on -- the cache
+    object, the batch, each sequence's packed-prefix length (changes at a rollover), the
+    selection capacity and the logits stride; a change recaptures."""
+
+    def __init__(self, engine: "FlashLoopEngine", use_graphs: bool) -> None:
+        self.engine = engine
+        self.use_graphs = bool(use_graphs)
+        self.reset()
+
+    def reset(self) -> None:
+        self.graph = None
+        self.key = None
+        self.tok = self.pos = self.logits = None
+
+    def _key(self, cache: CrossLoopKVCache, bsz: int) -> tuple:
+        lc = cache.layers[0]
+        cap = kernels.decode_capacity(lc.token_count + 1, self.engine.config.effective_decode_key_fraction)
+        return (id(cache), bsz, tuple(lc.packed_host), cap, lc.logits_capacity())
+
+    def step(self, cache: CrossLoopKVCache, token_ids: torch.Tensor, positions: Sequence[int]) -> torch.Tensor:
+        """Logits ``[B, vocab]`` of one step; the caller then commits the appends
+        (``commit_append`` on every layer)."""
+        eng = self.engine
+        bsz = token_ids.shape[0]
+        dev = token_ids.device
+        if not self.use_graphs:
+            pos_t = torch.tensor([[int(p)] for p in positions], dtype=torch.long, device=dev)
+            return eng._decode_core(cache, eng.backbone.embed_tokens(token_ids), pos_t)
+        if self.tok is None or self.tok.shape[0] != bsz:
+            self.tok = torch.zeros((bsz, 1), dtype=torch.long, device=dev)
+            self.pos = torch.zeros((bsz, 1), dtype=torch.long, device=dev)
+            self.graph = None
+        self.tok.copy_(token_ids)
+        if bsz == 1:
+            self.pos.fill_(int(positions[0]))
+        else:
+            self.pos.copy_(torch.tensor([[int(p)] for p in positions], dtype=torch.long), non_blocking=False)
+        key = self._key(cache, bsz)
+        if self.graph is None or self.key != key:
+            self.graph = None
+            self._capture(cache)
+            self.key = key
+        self.graph.replay()
+        return self.logits
+
+    def _capture(self, cache: CrossLoopKVCache) -> None:
+        """A warm-up run on a side stream first sizes every workspace and library handle;
+        its append is then undone on the device (the replay rewrites the same rows)."""
+        eng = self.engine
+        side = torch.cuda.Stream()  # default priority
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
+            for lc in cache.layers:
+                lc.tail_tokens -= 1
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
+        self.graph = graph
 
 
 class FlashLoopEngine:
@@ -99,13 +173,7 @@ class FlashLoopEngine:
         self.layers = model.model.layers
         self._state: EngineState | None = None
         self.observer: Callable[[str, dict], None] | None = None
-        # HIP-graph replay of decode steps (the per-layer launches of a step become one
-        # graph launch); off = eager launches
-        self.use_graphs = bool(use_graphs)
-        self._graph = None
-        self._graph_at = None
-        self._g_tok = self._g_pos = self._g_logits = None
-        self._g_counts: list[int] = []
+        self._runner = DecodeRunner(self, use_graphs)
 
     @classmethod
     def from_pretrained(cls, model_path: str, *, config: FlashLoopConfig | None = None,
@@ -124,16 +192,27 @@ class FlashLoopEngine:
             raise RuntimeError("engine cache is not initialized")
         return self._state
 
+    @property
+    def use_graphs(self) -> bool:
+        """Decode steps replay a captured HIP graph (True) or launch eagerly (False)."""
+        return self._runner.use_graphs
+
+    @use_graphs.setter
+    def use_graphs(self, on: bool) -> None:
+        self._runner.use_graphs = bool(on)
+        self._runner.reset()
+
     def reset(self) -> None:
         self._state = None
-        self._graph = None
-        self._graph_at = None
+        self._runner.reset()
 
     # ------------------------------------------------------------------ prefill
-    def _qkv(self, attn, x: torch.Tensor, rows: int):
-        q = attn.q_proj(x).view(1, rows, -1, attn.head_dim).transpose(1, 2)
-        k = attn.k_proj(x).view(1, rows, -1, attn.head_dim).transpose(1, 2)
-        v = attn.v_proj(x).view(1, rows, -1, attn.head_dim).transpose(1, 2)
+    def _qkv(self, attn, x: torch.Tensor):
+        """q, k, v ``[B, heads, S, head_dim]`` of hidden rows ``x`` ``[B, S, hidden]``."""
+        bsz, rows = x.shape[0], x.shape[1]
+        q = attn.q_proj(x).view(bsz, rows, -1, attn.head_dim).transpose(1, 2)
+        k = attn.k_proj(x).view(bsz, rows, -1, attn.head_dim).transpose(1, 2)
+        v = attn.v_proj(x).view(bsz, rows, -1, attn.head_dim).transpose(1, 2)
         return q, k, v
 
     def _dense_loop(self, hidden: torch.Tensor, cos, sin):
@@ -143,7 +222,7 @@ class FlashLoopEngine:
         h = hidden
         for layer in self.layers:
             a = layer.self_attn
-            q, k, v = self._qkv(a, layer.input_layernorm(h), t)
+            q, k, v = self._qkv(a, layer.input_layernorm(h))
             q, k = apply_rope(q, k, cos, sin)
             o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
             o = a.o_proj(o.transpose(1, 2).reshape(1, t, -1))
@@ -167,7 +246,7 @@ class FlashLoopEngine:
         for li, layer in enumerate(self.layers):
             a = layer.self_attn
             active, _ = kernels.gather_rows(h, positions, dim=1)
-            q, k, v = self._qkv(a, layer.input_layernorm(active), n)
+            q, k, v = self._qkv(a, layer.input_layernorm(active))
             q, k = apply_rope(q, k, cos_a, sin_a)
             full_k = prev_keys[li].clone()
             full_v = prev_values[li].clone()
@@ -191,6 +270,31 @@ class FlashLoopEngine:
         n = int(counts[0].item())  # prefill syncs once per loop boundary, as the reference does
         return mask, positions[0, :n].contiguous(), score
 
+    def _prefill_loops(self, input_ids: torch.Tensor, stage: Callable[[str], None] = lambda _n: None) -> "_PrefillLoops":
+        """The four prefill loops of one sequence ``[1, T]`` (flashloop/engine.py:176-333):
+        dense loops 1-2, then token-sparse loops 3-4 on the rows selected by the hidden
+        delta score.  Returns every layer's K/V of every loop, the masks and the logits."""
+        t = int(input_ids.shape[1])
+        dev = input_ids.device
+        hidden = self.backbone.embed_tokens(input_ids)
+        cos, sin = self.backbone.rotary_emb(hidden, torch.arange(t, device=dev)[None])
+        stage("inputs_ready")
+        h1, k1, v1 = self._dense_loop(hidden, cos, sin)
+        stage("loop1_dense")
+        h2, k2, v2 = self._dense_loop(h1, cos, sin)
+        stage("loop2_dense")
+        f3, f4 = self.config.effective_prefill_fractions
+        mask3, pos3, _ = self._select(h2, h1, f3)
+        h3, k3, v3 = self._sparse_loop(h2, pos3, k2, v2, cos, sin)
+        stage("loop3_sparse")
+        mask4, pos4, _ = self._select(h3, h2, f4, eligible=mask3)
+        h4, k4, v4 = self._sparse_loop(h3, pos4, k3, v3, cos, sin)
+        stage("loop4_sparse")
+        receipts = (PrefillReceipt(1, t, t), PrefillReceipt(2, t, t), PrefillReceipt(3, t, pos3.numel()),
+                    PrefillReceipt(4, t, pos4.numel()))
+        return _PrefillLoops([k1, k2, k3, k4], [v1, v2, v3, v4], mask3, mask4, receipts,
+                             self.model.lm_head(h4[:, -1]).float())
+
     @torch.inference_mode()
     def prefill(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None, *,
                 decode_capacity: int | None = None,
@@ -211,71 +315,53 @@ class FlashLoopEngine:
             raise ValueError("prefill requires at least one prompt token")
         if attention_mask is not None and (attention_mask.shape != input_ids.shape or not bool(attention_mask.bool().all())):
             raise ValueError("padding is not supported by the batch-one engine")
-        dev = input_ids.device
-        hidden = self.backbone.embed_tokens(input_ids)
-        cos, sin = self.backbone.rotary_emb(hidden, torch.arange(t, device=dev)[None])
-        stage("inputs_ready")
-        h1, k1, v1 = self._dense_loop(hidden, cos, sin)
-        stage("loop1_dense")
-        h2, k2, v2 = self._dense_loop(h1, cos, sin)
-        stage("loop2_dense")
-        f3, f4 = self.config.effective_prefill_fractions
-        mask3, pos3, _ = self._select(h2, h1, f3)
-        n3 = pos3.numel()
-        h3, k3, v3 = self._sparse_loop(h2, pos3, k2, v2, cos, sin)
-        stage("loop3_sparse")
-        mask4, pos4, _ = self._select(h3, h2, f4, eligible=mask3)
-        n4 = pos4.numel()
-        h4, k4, v4 = self._sparse_loop(h3, pos4, k3, v3, cos, sin)
-        stage("loop4_sparse")
+        loops = self._prefill_loops(input_ids, stage)
         cap = t + (self.config.decode_capacity if decode_capacity is None else int(decode_capacity))
         cache = CrossLoopKVCache(num_layers=len(self.layers))
         for li in range(len(self.layers)):
             cache.set_layer(li, CrossLoopKVLayer.from_prefill(
-                [k1[li], k2[li], k3[li], k4[li]], [v1[li], v2[li], v3[li], v4[li]],
-                mask_loop3=mask3, mask_loop4=mask4, token_capacity=cap))
+                [k[li] for k in loops.keys], [v[li] for v in loops.values],
+                mask_loop3=loops.mask3, mask_loop4=loops.mask4, token_capacity=cap))
         stage("physical_cache_finalized")
-        receipts = (PrefillReceipt(1, t, t), PrefillReceipt(2, t, t), PrefillReceipt(3, t, n3), PrefillReceipt(4, t, n4))
-        self._state = EngineState(cache, t, mask3, mask4, receipts)
-        self._graph = None  # a new cache: captured pointers are stale
-        logits = self.model.lm_head(h4[:, -1]).float()
+        self._state = EngineState(cache, t, loops.mask3, loops.mask4, loops.receipts)
+        self._runner.reset()  # a new cache: captured pointers are stale
+        logits = loops.logits
         stage("logits_ready")
         return PrefillOutput(logits=logits, state=self._state)
 
     # ------------------------------------------------------------------ decode
-    def _decode_core(self, h: torch.Tensor, pos_t: torch.Tensor, pos: int) -> tuple[torch.Tensor, list[int]]:
-        """One decode step on the device: every layer and loop, then the cache appends
-        (device tail lengths, no host index).  ``pos_t`` holds the position on the device
-        (``pos`` only feeds host-side receipts).  Returns (logits, selected counts)."""
-        state = self.state
+    def _decode_core(self, cache: CrossLoopKVCache, h: torch.Tensor, pos_t: torch.Tensor) -> torch.Tensor:
+        """One decode step of ``B`` sequences on the device: every layer and loop, then the
+        cache appends (device tail lengths, no host index).  ``h``: embedded tokens
+        ``[B, 1, hidden]``; ``pos_t``: their positions ``[B, 1]`` on the device.  Returns
+        the logits ``[B, vocab]``.  Host values it reads (prefix lengths, the selection
+        capacity) change only at a rollover or a capacity step, so it can be captured."""
         cfg = self.config
         sparse = cfg.enable_sparse_decode
         fraction = cfg.effective_decode_key_fraction
+        bsz = h.shape[0]
         cos, sin = self.backbone.rotary_emb(h, pos_t)
         nl = len(self.layers)
         cur_k = [[None] * 4 for _ in range(nl)]
         cur_v = [[None] * 4 for _ in range(nl)]
         sources: list[_LayerSource | None] = [None] * nl
-        counts: list[int] = []
         for loop in range(4):
             for li, layer in enumerate(self.layers):
                 a = layer.self_attn
                 residual = h
-                q, k, v = self._qkv(a, layer.input_layernorm(h), 1)
+                q, k, v = self._qkv(a, layer.input_layernorm(h))
                 q, k = apply_rope(q, k, cos, sin)
                 q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
                 cur_k[li][loop] = k
                 cur_v[li][loop] = v
-                lc = state.cache.layers[li]
+                lc = cache.layers[li]
                 if loop < 2 or not sparse:
                     out, lg = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
                                                         scaling=a.scaling, return_logits=(loop == 1 and sparse))
-                    projected = a.o_proj(out.to(q.dtype).transpose(1, 2).reshape(1, 1, -1))
+                    projected = a.o_proj(out.to(q.dtype).transpose(1, 2).reshape(bsz, 1, -1))
                     if loop == 1 and sparse:
-                        idx, valid, mass, w, cnt = lc.select_decode_keys(lg, fraction)
-                        sources[li] = _LayerSource(projected, idx, valid, mass, w, v,
-                                                   count=min(pos + 1, _budget(pos + 1, fraction)))
-                        counts.append(sources[li].count)
+                        idx, valid, mass, w, _ = lc.select_decode_keys(lg, fraction)
+                        sources[li] = _LayerSource(projected, idx, valid, mass, w, v)
                 else:
                     src = sources[li]
                     if src.selected_output is None:
@@ -289,55 +375,28 @@ class FlashLoopEngine:
                             loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
                             source_selected_output=src.selected_output, global_mass=src.global_mass,
                             scaling=a.scaling)
-                    projected = src.projected_output + a.o_proj(delta.to(v.dtype).transpose(1, 2).reshape(1, 1, -1))
+                    projected = src.projected_output + a.o_proj(
+                        delta.to(v.dtype).transpose(1, 2).reshape(bsz, 1, -1))
                 h = residual + layer.input_layernorm_2(projected)
                 h = h + layer.post_attention_layernorm_2(layer.mlp(layer.post_attention_layernorm(h)))
             h = self.backbone.norm(h)
         for li in range(nl):
-            state.cache.layers[li].append_rows(cur_k[li], cur_v[li])
-        return self.model.lm_head(h[:, -1]).float(), counts
+            cache.layers[li].append_rows(cur_k[li], cur_v[li])
+        return self.model.lm_head(h[:, -1]).float()
 
-    def _finish_step(self, logits: torch.Tensor, counts: list[int]) -> DecodeOutput:
-        state = self.state
-        for lc in state.cache.layers:
-            lc.commit_append()  # host mirrors; rolls a group out of full tails (outside any graph)
-        self._state = EngineState(state.cache, state.next_position + 1, state.mask_loop3, state.mask_loop4,
-                                  state.prefill_receipts)
+    def _receipt(self, positions: Sequence[int]) -> DecodeReceipt:
         nl = len(self.layers)
         sparse = self.config.enable_sparse_decode
-        receipt = DecodeReceipt(
+        fraction = self.config.effective_decode_key_fraction
+        # keys selected per layer (of the first sequence; all layers select the same count)
+        n = positions[0] + 1
+        counts = (min(n, _budget(n, fraction)),) * nl if sparse else ()
+        return DecodeReceipt(
             dense_attention_calls=(2 if sparse else 4) * nl,
             sparse_attention_calls=(2 if sparse else 0) * nl,
             dense_late_loop_calls=(0 if sparse else 2) * nl,
-            selected_keys_per_layer=tuple(counts),
+            selected_keys_per_layer=counts,
         )
-        return DecodeOutput(logits=logits, state=self._state, receipt=receipt)
-
-    def _graph_key(self) -> tuple:
-        """Host-side values a captured step depends on: prefix lengths (rollover), the
-        selection capacity and the logits stride."""
-        lc = self.state.cache.layers[0]
-        cap = kernels.decode_capacity(lc.token_count + 1, self.config.effective_decode_key_fraction)
-        return (tuple(lc.packed_host), cap, lc.logits_capacity())
-
-    def _capture(self) -> None:
-        """Capture one decode step in a HIP graph.  A warm-up run on a side stream first sizes
-        every workspace and library handle; its append is then undone on the device (the
-        replay rewrites the same rows)."""
-        tok, pos_t = self._g_tok, self._g_pos
-        pos = self.state.next_position
-        side = torch.cuda.Stream()  # default priority
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            self._decode_core(self.backbone.embed_tokens(tok), pos_t, pos)
-            for lc in self.state.cache.layers:
-                lc.tail_tokens -= 1
-        torch.cuda.current_stream().wait_stream(side)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            logits, counts = self._decode_core(self.backbone.embed_tokens(tok), pos_t, pos)
-        self._graph, self._g_logits, self._g_counts = graph, logits, counts
-        self._graph_at = self._graph_key()
 
     @torch.inference_mode()
     def decode(self, token_ids: torch.Tensor) -> DecodeOutput:
@@ -349,23 +408,11 @@ class FlashLoopEngine:
         if token_ids.shape != (1, 1):
             raise ValueError("decode requires exactly one token at batch size one")
         pos = state.next_position
-        if not self.use_graphs:
-            h = self.backbone.embed_tokens(token_ids)
-            pos_t = torch.tensor([[pos]], device=h.device)
-            logits, counts = self._decode_core(h, pos_t, pos)
-            return self._finish_step(logits, counts)
-        if self._g_tok is None:
-            self._g_tok = torch.zeros((1, 1), dtype=torch.long, device=token_ids.device)
-            self._g_pos = torch.zeros((1, 1), dtype=torch.long, device=token_ids.device)
-        self._g_tok.copy_(token_ids)
-        self._g_pos.fill_(pos)
-        if self._graph is None or self._graph_at != self._graph_key():
-            self._graph = None
-            self._capture()
-        self._graph.replay()
-        fraction = self.config.effective_decode_key_fraction
-        counts = [min(pos + 1, _budget(pos + 1, fraction))] * len(self._g_counts)
-        return self._finish_step(self._g_logits, counts)
+        logits = self._runner.step(state.cache, token_ids, [pos])
+        for lc in state.cache.layers:
+            lc.commit_append()  # host mirrors; rolls a group out of full tails (outside any graph)
+        self._state = EngineState(state.cache, pos + 1, state.mask_loop3, state.mask_loop4, state.prefill_receipts)
+        return DecodeOutput(logits=logits, state=self._state, receipt=self._receipt([pos]))
 
     # ------------------------------------------------------------------ generate
     @torch.inference_mode()

@@ -84,18 +84,38 @@ class CrossLoopKVQuantizationIntervention:
         first = layers[0]
         storage = sum(l.storage_bytes for l in layers)
         dense = sum(l.dense_bf16_bytes for l in layers)
+        h = first.heads
+        tails = sum(first.tail_host)
+        # kv_quantization.py:246-322 field by field: packed streams (codes + fp32 metadata
+        # + rank maps), the BF16 tails of every loop, and the two prefill masks as bits
+        tail_bytes = len(layers) * 4 * 2 * h * tails * 128 * 2
+        st = self.engine.state
+        mask_bytes = -(-2 * int(st.mask_loop3.numel()) // 8) if st.mask_loop3 is not None else 0
+        packed_stream_bytes = storage - tail_bytes
         return {
             "status": "PASS",
             "kind": "asymmetric_cross_loop_innovation_int4",
             "codec_profile": "kivi4_channel",
+            "recurrent_steps": 4,
+            "key_axes": ["per_channel"] * 4,
+            "value_axes": ["per_token"] * 4,
+            "k_bits": [4] * 4,
+            "v_bits": [4] * 4,
             "group_size": 64,
             "residual_length": 64,
-            "quantized_groups": sum(l.quantized_tokens // 64 for l in layers),
+            "quantized_groups": sum(sum(l.packed_host) // 64 for l in layers),
             "quantized_tokens": first.quantized_tokens,
             "bf16_tail_tokens": first.tail_tokens_max,
-            "total_packed_bytes": storage,
+            "total_cache_tokens": first.token_count,
+            "current_cache_tokens": first.token_count,
+            "packed_stream_bytes": packed_stream_bytes,
+            "residual_bf16_bytes": tail_bytes,
+            "mask_bytes": mask_bytes,
+            "total_packed_bytes": storage + mask_bytes,
+            "dense_recurrent_bf16_bytes": dense,
             "dense_r4_bf16_bytes": dense,
-            "dense_r4_ratio": storage / dense if dense else None,
+            "dense_recurrent_ratio": (storage + mask_bytes) / dense if dense else None,
+            "dense_r4_ratio": (storage + mask_bytes) / dense if dense else None,
             "reference_cache_materialized": False,
             **base,
         }

@@ -100,6 +100,8 @@ def test_generate_crosses_rollover_and_hooks():
         joint = hooks["attention_and_prefill"].audit()
     assert torch.equal(out, out2)
     assert audit["status"] == "PASS" and audit["quantized_tokens"] == 192
+    assert audit["quantized_groups"] == TINY.num_hidden_layers * 192 // 64
+    assert audit["packed_stream_bytes"] + audit["residual_bf16_bytes"] + audit["mask_bytes"] == audit["total_packed_bytes"]
     assert joint["token_sparse_prefill"]["mask_nested"]
     assert joint["attention"]["target_replacements"] == 2 * TINY.num_hidden_layers * 69
     assert model.generate.__func__ is OuroForCausalLM.generate
@@ -120,9 +122,9 @@ def test_graph_decode_matches_eager():
     for i in range(600, 700):
         tok = ids[:, i:i + 1]
         da = eager.decode(tok)
-        before = graphed._graph
+        before = graphed._runner.graph
         db = graphed.decode(tok)
-        captures += graphed._graph is not before
+        captures += graphed._runner.graph is not before
         assert torch.equal(da.logits, db.logits), f"step {i}"
         assert da.receipt == db.receipt
     assert captures >= 3  # first capture, rollovers at 640 and 704-64, capacity step at 640
@@ -131,3 +133,24 @@ def test_graph_decode_matches_eager():
     for s in range(4):
         assert torch.equal(la.codes[s], lb.codes[s])
         assert torch.equal(la.tail_key[s], lb.tail_key[s])
+
+
+def test_saved_cache_decodes_identically(tmp_path):
+    """A prefilled cache written to disk and read back decodes to the same logits."""
+    from flashloop_amd.cache import CrossLoopKVCache
+
+    model = OuroForCausalLM.random_init(TINY, seed=8, device="cuda")
+    ids = _ids(300, seed=8)
+    a = FlashLoopEngine(model, use_graphs=False)
+    b = FlashLoopEngine(model, use_graphs=False)
+    a.prefill(ids[:, :290], decode_capacity=32)
+    b.prefill(ids[:, :290], decode_capacity=32)
+    path = str(tmp_path / "kv.safetensors")
+    a.state.cache.save(path)
+    loaded = CrossLoopKVCache.load(path, device="cuda")
+    st = b.state
+    b._state = type(st)(loaded, st.next_position, st.mask_loop3, st.mask_loop4, st.prefill_receipts)
+    for i in range(290, 300):
+        da = a.decode(ids[:, i:i + 1])
+        db = b.decode(ids[:, i:i + 1])
+        assert torch.equal(da.logits, db.logits), f"step {i}"

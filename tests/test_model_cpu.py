@@ -51,3 +51,19 @@ def test_dense_forward_is_causal():
     full = m.dense_forward(ids[:, :11])
     again = m.dense_forward(ids[:, :11].clone())
     assert torch.equal(full, again)
+
+
+def test_batch_engine_lengths_validation():
+    import pytest as _pt
+    import torch as _t
+
+    from flashloop_amd.batch_engine import FlashLoopBatchEngine
+
+    ids = _t.zeros(3, 5, dtype=_t.long)
+    assert FlashLoopBatchEngine._lengths(ids, None) == [5, 5, 5]
+    m = _t.tensor([[1, 1, 1, 0, 0], [1, 1, 1, 1, 1], [1, 0, 0, 0, 0]])
+    assert FlashLoopBatchEngine._lengths(ids, m) == [3, 5, 1]
+    with _pt.raises(ValueError, match="right-padded"):
+        FlashLoopBatchEngine._lengths(ids, _t.tensor([[0, 1, 1, 1, 1]] * 3))
+    with _pt.raises(ValueError, match="no tokens"):
+        FlashLoopBatchEngine._lengths(ids, _t.zeros(3, 5))
