@@ -77,6 +77,8 @@ SIGNATURES = {
     "fl_scatter_rows": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "fl_hidden_delta_score": (_I32, [_P, _P, _I64, _I32, _P, _P]),
     "fl_select_tokens": (_I32, [_P, _I32, _I32, _F64, _P, _I32, _P, _P, _P, _P, _P]),
+    "fl_gemv_bf16": (_I32, [_P, _I32, _I64, _I32, _I32, _PP, _I32, _I32, _PP, _I64, _P, _I64, _P, _P, _I32, _P]),
+    "fl_norm_chain": (_I32, [_I32, _I32, _F32, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
 }
 
 _lib: C.CDLL | None = None

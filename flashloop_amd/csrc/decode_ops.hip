@@ -1,0 +1,407 @@
+// Decode-step model kernels: the per-layer work around the cache readers, fused so that
+// one decode step of a layer and loop is eight launches instead of ~60 (the step of
+// flashloop/engine.py:396-537 on an Ouro-shaped sandwich-norm layer).
+//
+//  * fl_gemv_bf16 -- y[m, n] = sum_k x[m, k] * W[n, k] for m < M <= 8 (nn.Linear weights,
+//    bf16, row-major [N, K]); fp32 accumulation; epilogues: plain bf16 out, f32 out of the
+//    bf16-rounded value (lm_head(...).float()), + bf16 addend, SwiGLU of a gate and an up
+//    matrix, or rotary embedding of q/k (and a plain v) from three matrices at once.
+//  * fl_norm_chain -- the residual/RMSNorm chain between two GEMVs of one row:
+//    h = r + n_a(x); optionally h = n_f(h); z = n_b(h).
+//
+// Every rounding to bf16 happens where the torch modules round (Linear output, RMSNorm
+// output, each binary op of rotate-half RoPE, SiLU, the SwiGLU product, residual adds).
+//
+// GEMV work split: a workgroup of kGemvWaves waves owns kRows output rows and splits K
+// between its waves (each wave streams 64 contiguous 16-byte chunks of each row per
+// step); the waves reduce their partial dots in registers (DPP) and combine through LDS.
+// The grid has N / kRows workgroups (>= 512 for every matrix of the model), so every CU
+// has several row blocks of weights in flight.  Memory-bound: bytes = N * K * 2 + M * K.
+#include "fl_common.h"
+
+namespace fl {
+namespace {
+
+constexpr int kGemvWaves = 4;
+constexpr int kGemvThreads = kGemvWaves * kWave;
+constexpr int kRows = 4;  // output rows per workgroup
+constexpr int kMaxM = 8;
+
+enum GemvEpi : int { kEpiPlain = 0, kEpiF32 = 1, kEpiAdd = 2, kEpiSwiGlu = 3, kEpiRope = 4 };
+
+struct GemvArgs {
+  const void* x;  // [M, K] bf16, or f32 (rounded to bf16 on load) when x_f32
+  int64_t x_stride;
+  int x_f32;
+  int M, K, N;  // N: rows of each matrix
+  const uint16_t* w[3];  // plain/add/f32: w[0]; swiglu: gate w[0], up w[1]; rope: q, k, v
+  void* y[3];            // outputs [M, N] (row stride y_stride); rope: q, k, v
+  int64_t y_stride;
+  const uint16_t* addend;  // kEpiAdd: [M, N] bf16 (row stride addend_stride)
+  int64_t addend_stride;
+  const uint16_t* cos;  // kEpiRope: [M, 128] bf16 tables of each row's position
+  const uint16_t* sin;
+  int head_dim;
+};
+
+__device__ __forceinline__ float bf16_round(float v) { return round_bf16(v); }
+
+__device__ __forceinline__ void unpack8(const uint4& u, float* f) {
+  f[0] = bf16lo_to_f32(u.x);
+  f[1] = bf16hi_to_f32(u.x);
+  f[2] = bf16lo_to_f32(u.y);
+  f[3] = bf16hi_to_f32(u.y);
+  f[4] = bf16lo_to_f32(u.z);
+  f[5] = bf16hi_to_f32(u.z);
+  f[6] = bf16lo_to_f32(u.w);
+  f[7] = bf16hi_to_f32(u.w);
+}
+
+// x chunk q (8 values) of row m, as the bf16 values the Linear sees
+template <bool XF32>
+__device__ __forceinline__ void load_x8(const GemvArgs& a, int m, int q, float* f) {
+  if (XF32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + m * a.x_stride + 8 * q);
+    const float4 u = p[0], v = p[1];
+    f[0] = bf16_round(u.x);
+    f[1] = bf16_round(u.y);
+    f[2] = bf16_round(u.z);
+    f[3] = bf16_round(u.w);
+    f[4] = bf16_round(v.x);
+    f[5] = bf16_round(v.y);
+    f[6] = bf16_round(v.z);
+    f[7] = bf16_round(v.w);
+  } else {
+    unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + m * a.x_stride + 8 * q), f);
+  }
+}
+
+// Rows of workgroup g.  Plain: 4 consecutive rows of w[0].  SwiGLU: 2 consecutive rows,
+// each of the gate and of the up matrix.  RoPE: matrix g / (N/4); within it the rotary
+// pair rows {c, c+1, c+64, c+65} of one head, c even < 64.
+template <int EPI>
+__device__ __forceinline__ void block_rows(const GemvArgs& a, int g, const uint16_t** rp, int* mat, int* n0) {
+  if (EPI == kEpiSwiGlu) {
+    const int n = 2 * g;
+    rp[0] = a.w[0] + static_cast<int64_t>(n) * a.K;
+    rp[1] = a.w[0] + static_cast<int64_t>(n + 1) * a.K;
+    rp[2] = a.w[1] + static_cast<int64_t>(n) * a.K;
+    rp[3] = a.w[1] + static_cast<int64_t>(n + 1) * a.K;
+    *mat = 0;
+    *n0 = n;
+  } else if (EPI == kEpiRope) {
+    const int per = a.N / kRows;
+    const int m = g / per, gi = g - m * per;
+    const int half = a.head_dim / 2, pairs = half / 2;  // row groups per head
+    const int head = gi / pairs, c = 2 * (gi - head * pairs);
+    const int n = head * a.head_dim + c;
+    const uint16_t* w = a.w[m];
+    rp[0] = w + static_cast<int64_t>(n) * a.K;
+    rp[1] = w + static_cast<int64_t>(n + 1) * a.K;
+    rp[2] = w + static_cast<int64_t>(n + half) * a.K;
+    rp[3] = w + static_cast<int64_t>(n + half + 1) * a.K;
+    *mat = m;
+    *n0 = n;
+  } else {
+    const int n = kRows * g;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) rp[r] = a.w[0] + static_cast<int64_t>(n + r) * a.K;
+    *mat = 0;
+    *n0 = n;
+  }
+}
+
+template <int MT, int EPI, bool XF32>
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
+  __shared__ float red[kGemvWaves][MT][kRows];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint16_t* rp[kRows];
+  int mat, n0;
+  block_rows<EPI>(a, blockIdx.x, rp, &mat, &n0);
+  float acc[MT][kRows];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) acc[m][r] = 0.0f;
+  const int nq = a.K / 8;  // 16-byte chunks per row
+  // chunk q = j*256 + wave*64 + lane: each wave reads 1 KB contiguous per row and step
+  constexpr int kStep = kGemvWaves * kWave;
+  int q = wave * kWave + lane;
+  // two steps per iteration keep 8 row loads in flight per lane
+  for (; q + kStep < nq; q += 2 * kStep) {
+    uint4 w0[kRows], w1[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      w0[r] = reinterpret_cast<const uint4*>(rp[r])[q];
+      w1[r] = reinterpret_cast<const uint4*>(rp[r])[q + kStep];
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < a.M) {
+        float x0[8], x1[8];
+        load_x8<XF32>(a, m, q, x0);
+        load_x8<XF32>(a, m, q + kStep, x1);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+          float f[8];
+          unpack8(w0[r], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x0[e], f[e], acc[m][r]);
+          unpack8(w1[r], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x1[e], f[e], acc[m][r]);
+        }
+      }
+    }
+  }
+  if (q < nq) {
+    uint4 w0[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) w0[r] = reinterpret_cast<const uint4*>(rp[r])[q];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < a.M) {
+        float x0[8];
+        load_x8<XF32>(a, m, q, x0);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+          float f[8];
+          unpack8(w0[r], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x0[e], f[e], acc[m][r]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      const float s = wave_sum(acc[m][r]);
+      if (lane == 0) red[wave][m][r] = s;
+    }
+  __syncthreads();
+  if (wave != 0 || lane >= a.M) return;
+  const int m = lane;
+  float v[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kGemvWaves; ++w) s += red[w][m < MT ? m : 0][r];
+    v[r] = bf16_round(s);  // the Linear's bf16 output
+  }
+  const int64_t yo = static_cast<int64_t>(m) * a.y_stride + n0;
+  if (EPI == kEpiF32) {
+    float* y = static_cast<float*>(a.y[0]) + yo;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) y[r] = v[r];
+  } else if (EPI == kEpiPlain || EPI == kEpiAdd) {
+    uint16_t* y = static_cast<uint16_t*>(a.y[0]) + yo;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      float o = v[r];
+      if (EPI == kEpiAdd) o = o + bf16_to_f32(a.addend[static_cast<int64_t>(m) * a.addend_stride + n0 + r]);
+      y[r] = f32_to_bf16_rne(o);
+    }
+  } else if (EPI == kEpiSwiGlu) {
+    // silu(gate) rounds to bf16 (F.silu on bf16), then the product rounds
+    uint16_t* y = static_cast<uint16_t*>(a.y[0]) + yo;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float g = v[r], u = v[2 + r];
+      const float s = bf16_round(g / (1.0f + expf(-g)));
+      y[r] = f32_to_bf16_rne(s * u);
+    }
+  } else {  // rope: rows (c, c+1) and (c+64, c+65); rotate_half(x)[c] = -x[c+64], [c+64] = x[c]
+    uint16_t* y = static_cast<uint16_t*>(a.y[mat]) + yo;
+    const int half = a.head_dim / 2;
+    if (mat == 2) {
+      y[0] = f32_to_bf16_rne(v[0]);
+      y[1] = f32_to_bf16_rne(v[1]);
+      y[half] = f32_to_bf16_rne(v[2]);
+      y[half + 1] = f32_to_bf16_rne(v[3]);
+    } else {
+      const int c = (n0 % a.head_dim);
+      const uint16_t* cs = a.cos + static_cast<int64_t>(m) * a.head_dim;
+      const uint16_t* sn = a.sin + static_cast<int64_t>(m) * a.head_dim;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float lo = v[e], hi = v[2 + e];
+        const float cl = bf16_to_f32(cs[c + e]), sl = bf16_to_f32(sn[c + e]);
+        const float ch = bf16_to_f32(cs[c + half + e]), sh = bf16_to_f32(sn[c + half + e]);
+        y[e] = f32_to_bf16_rne(bf16_round(lo * cl) + bf16_round(-hi * sl));
+        y[half + e] = f32_to_bf16_rne(bf16_round(hi * ch) + bf16_round(lo * sh));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Residual / RMSNorm chain of one row (one workgroup per row, 256 threads, D <= 8192).
+// RMSNorm(x) = bf16(w * (x * rsqrt(mean(x^2) + eps))) in fp32, as the model's module.
+constexpr int kNormThreads = 256;
+constexpr int kNormPer = 32;  // values per thread (D <= 8192)
+
+struct NormArgs {
+  int D;
+  float eps;
+  const uint16_t* x;   // [M, D] or null (then h = r)
+  const uint16_t* r;   // [M, D] residual / input
+  const uint16_t* wa;  // norm of x
+  const uint16_t* wf;  // optional norm of h (replaces h)
+  const uint16_t* wb;  // optional norm of h -> z
+  uint16_t* h_out;     // optional
+  uint16_t* z_out;     // optional
+  int64_t stride;      // row stride of every [M, D] tensor
+};
+
+__device__ float norm_block_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / kWave; ++i) s += red[i];
+  return s;
+}
+
+// vals <- RMSNorm(vals) with weight w, rounded to bf16
+__device__ __forceinline__ void rms_apply(float* vals, int n_mine, const uint16_t* w, int D, float eps, float* red) {
+  float ss = 0.0f;
+  for (int i = 0; i < n_mine; ++i) ss = fmaf(vals[i], vals[i], ss);
+  const float ms = norm_block_sum(ss, red) / static_cast<float>(D);
+  const float inv = rsqrtf(ms + eps);
+  for (int i = 0; i < n_mine; ++i) {
+    const int c = threadIdx.x + i * kNormThreads;
+    vals[i] = bf16_round(bf16_to_f32(w[c]) * (vals[i] * inv));
+  }
+}
+
+__global__ __launch_bounds__(kNormThreads) void norm_chain_kernel(NormArgs a) {
+  __shared__ float red[kNormThreads / kWave];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * a.stride;
+  const int n_mine = (a.D - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;
+  float hv[kNormPer];
+  if (a.x != nullptr) {
+    float xv[kNormPer];
+#pragma unroll
+    for (int i = 0; i < kNormPer; ++i)
+      if (i < n_mine) xv[i] = bf16_to_f32(a.x[base + threadIdx.x + i * kNormThreads]);
+    rms_apply(xv, n_mine, a.wa, a.D, a.eps, red);
+#pragma unroll
+    for (int i = 0; i < kNormPer; ++i)
+      if (i < n_mine) hv[i] = bf16_round(bf16_to_f32(a.r[base + threadIdx.x + i * kNormThreads]) + xv[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kNormPer; ++i)
+      if (i < n_mine) hv[i] = bf16_to_f32(a.r[base + threadIdx.x + i * kNormThreads]);
+  }
+  if (a.wf != nullptr) rms_apply(hv, n_mine, a.wf, a.D, a.eps, red);
+  if (a.h_out != nullptr) {
+#pragma unroll
+    for (int i = 0; i < kNormPer; ++i)
+      if (i < n_mine) a.h_out[base + threadIdx.x + i * kNormThreads] = f32_to_bf16_rne(hv[i]);
+  }
+  if (a.wb != nullptr) {
+    rms_apply(hv, n_mine, a.wb, a.D, a.eps, red);
+#pragma unroll
+    for (int i = 0; i < kNormPer; ++i)
+      if (i < n_mine) a.z_out[base + threadIdx.x + i * kNormThreads] = f32_to_bf16_rne(hv[i]);
+  }
+}
+
+template <int MT, int EPI>
+void launch_gemv_m(const GemvArgs& a, int blocks, hipStream_t st) {
+  if (a.x_f32)
+    hipLaunchKernelGGL((gemv_kernel<MT, EPI, true>), dim3(blocks), dim3(kGemvThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemv_kernel<MT, EPI, false>), dim3(blocks), dim3(kGemvThreads), 0, st, a);
+}
+
+template <int EPI>
+void launch_gemv(const GemvArgs& a, int blocks, hipStream_t st) {
+  if (a.M <= 1)
+    launch_gemv_m<1, EPI>(a, blocks, st);
+  else if (a.M <= 2)
+    launch_gemv_m<2, EPI>(a, blocks, st);
+  else if (a.M <= 4)
+    launch_gemv_m<4, EPI>(a, blocks, st);
+  else
+    launch_gemv_m<8, EPI>(a, blocks, st);
+}
+
+}  // namespace
+}  // namespace fl
+
+extern "C" int32_t fl_gemv_bf16(const void* x, int32_t x_is_f32, int64_t x_stride, int32_t m, int32_t k,
+                                const uint16_t* const* weights, int32_t n, int32_t epilogue, void* const* outputs,
+                                int64_t out_stride, const uint16_t* addend, int64_t addend_stride,
+                                const uint16_t* rope_cos, const uint16_t* rope_sin, int32_t head_dim, void* stream) {
+  using namespace fl;
+  clear_error();
+  FL_REQUIRE(x && weights && outputs, "fl_gemv_bf16: null x/weights/outputs");
+  FL_REQUIRE(m >= 1 && m <= kMaxM, "fl_gemv_bf16: rows of x must be 1..8");
+  FL_REQUIRE(k > 0 && k % 8 == 0 && n > 0 && n % kRows == 0, "fl_gemv_bf16: K must be a multiple of 8, N of 4");
+  FL_REQUIRE(x_stride >= k && out_stride >= n, "fl_gemv_bf16: bad row strides");
+  FL_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && (x_stride * (x_is_f32 ? 4 : 2)) % 16 == 0,
+             "fl_gemv_bf16: x rows must be 16-byte aligned");
+  FL_REQUIRE(epilogue >= kEpiPlain && epilogue <= kEpiRope, "fl_gemv_bf16: unknown epilogue");
+  const int nmat = epilogue == kEpiRope ? 3 : (epilogue == kEpiSwiGlu ? 2 : 1);
+  GemvArgs a{};
+  for (int i = 0; i < nmat; ++i) {
+    FL_REQUIRE(weights[i] != nullptr && reinterpret_cast<uintptr_t>(weights[i]) % 16 == 0,
+               "fl_gemv_bf16: weights must be non-null and 16-byte aligned");
+    a.w[i] = weights[i];
+  }
+  const int nout = epilogue == kEpiRope ? 3 : 1;
+  for (int i = 0; i < nout; ++i) {
+    FL_REQUIRE(outputs[i] != nullptr, "fl_gemv_bf16: null output");
+    a.y[i] = outputs[i];
+  }
+  if (epilogue == kEpiAdd) FL_REQUIRE(addend != nullptr && addend_stride >= n, "fl_gemv_bf16: bad addend");
+  if (epilogue == kEpiSwiGlu) FL_REQUIRE(n % 2 == 0, "fl_gemv_bf16: SwiGLU needs an even N");
+  if (epilogue == kEpiRope)
+    FL_REQUIRE(rope_cos && rope_sin && head_dim >= 8 && head_dim % 8 == 0 && n % head_dim == 0,
+               "fl_gemv_bf16: rope needs cos/sin tables and N a multiple of head_dim (multiple of 8)");
+  a.x = x;
+  a.x_f32 = x_is_f32 ? 1 : 0;
+  a.x_stride = x_stride;
+  a.M = m;
+  a.K = k;
+  a.N = n;
+  a.y_stride = out_stride;
+  a.addend = addend;
+  a.addend_stride = addend_stride;
+  a.cos = rope_cos;
+  a.sin = rope_sin;
+  a.head_dim = head_dim;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (epilogue) {
+    case kEpiPlain: launch_gemv<kEpiPlain>(a, n / kRows, st); break;
+    case kEpiF32: launch_gemv<kEpiF32>(a, n / kRows, st); break;
+    case kEpiAdd: launch_gemv<kEpiAdd>(a, n / kRows, st); break;
+    case kEpiSwiGlu: launch_gemv<kEpiSwiGlu>(a, n / 2, st); break;
+    default: launch_gemv<kEpiRope>(a, 3 * (n / kRows), st); break;
+  }
+  FL_LAUNCH_CHECK("fl_gemv_bf16");
+  return FL_OK;
+}
+
+extern "C" int32_t fl_norm_chain(int32_t m, int32_t d, float eps, const uint16_t* x, const uint16_t* r,
+                                 const uint16_t* w_a, const uint16_t* w_f, const uint16_t* w_b, uint16_t* h_out,
+                                 uint16_t* z_out, int64_t stride, void* stream) {
+  using namespace fl;
+  clear_error();
+  FL_REQUIRE(m >= 0 && d > 0 && d <= kNormThreads * kNormPer && stride >= d, "fl_norm_chain: bad shape");
+  FL_REQUIRE(r != nullptr, "fl_norm_chain: null residual/input");
+  FL_REQUIRE(x == nullptr || w_a != nullptr, "fl_norm_chain: x needs its norm weight");
+  FL_REQUIRE(w_b == nullptr || z_out != nullptr, "fl_norm_chain: z needs an output");
+  FL_REQUIRE(h_out != nullptr || z_out != nullptr, "fl_norm_chain: nothing to write");
+  if (m == 0) return FL_OK;
+  NormArgs a{d, eps, x, r, w_a, w_f, w_b, h_out, z_out, stride};
+  hipLaunchKernelGGL(norm_chain_kernel, dim3(m), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream), a);
+  FL_LAUNCH_CHECK("fl_norm_chain");
+  return FL_OK;
+}

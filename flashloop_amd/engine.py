@@ -17,6 +17,7 @@ Model GEMMs, norms and SDPA of the dense prefill loops are torch (hipBLASLt).
 
 from __future__ import annotations
 
+import gc
 import math
 from dataclasses import dataclass, field
 from typing import Callable, Sequence
@@ -156,8 +157,15 @@ class DecodeRunner:
                 lc.tail_tokens -= 1
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
+        # No garbage collection while capturing: a collected cycle can hold an earlier
+        # graph or its memory pool, whose release is illegal inside a capture.
+        gc.collect()
+        gc.disable()
+        try:
+            with torch.cuda.graph(graph):
+                self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
+        finally:
+            gc.enable()
         self.graph = graph
 
 
@@ -174,6 +182,9 @@ class FlashLoopEngine:
         self._state: EngineState | None = None
         self.observer: Callable[[str, dict], None] | None = None
         self._runner = DecodeRunner(self, use_graphs)
+        # decode-step model ops on the fused HIP kernels (False: torch modules)
+        self.fused_decode = True
+        self._wcache = None
 
     @classmethod
     def from_pretrained(cls, model_path: str, *, config: FlashLoopConfig | None = None,
@@ -331,6 +342,99 @@ class FlashLoopEngine:
 
     # ------------------------------------------------------------------ decode
     def _decode_core(self, cache: CrossLoopKVCache, h: torch.Tensor, pos_t: torch.Tensor) -> torch.Tensor:
+        """One decode step (see ``_decode_core_fused``); the torch-module form runs when the
+        fused kernels do not apply (``fused_decode`` off, non-bf16 weights, batch > 8)."""
+        if self.fused_decode and h.shape[0] <= 8 and self._fused_weights() is not None:
+            return self._decode_core_fused(cache, h, pos_t)
+        return self._decode_core_modules(cache, h, pos_t)
+
+    def _fused_weights(self):
+        """Per-layer weight tensors of the fused decode path, or None when a weight is not a
+        contiguous bf16 device tensor."""
+        if self._wcache is None:
+            def ok(t):
+                return t.dtype == torch.bfloat16 and t.is_cuda and t.is_contiguous()
+
+            layers = []
+            for layer in self.layers:
+                a, m = layer.self_attn, layer.mlp
+                w = dict(q=a.q_proj.weight, k=a.k_proj.weight, v=a.v_proj.weight, o=a.o_proj.weight,
+                         gate=m.gate_proj.weight, up=m.up_proj.weight, down=m.down_proj.weight,
+                         ln1=layer.input_layernorm.weight, ln2=layer.input_layernorm_2.weight,
+                         ln3=layer.post_attention_layernorm.weight, ln4=layer.post_attention_layernorm_2.weight)
+                if not all(ok(t) for t in w.values()) or a.num_key_value_heads != a.num_heads:
+                    self._wcache = False
+                    return None
+                layers.append(w)
+            extra = dict(norm=self.backbone.norm.weight, lm_head=self.model.lm_head.weight)
+            self._wcache = (layers, extra) if all(ok(t) for t in extra.values()) else False
+        return self._wcache or None
+
+    def _decode_core_fused(self, cache: CrossLoopKVCache, h: torch.Tensor, pos_t: torch.Tensor) -> torch.Tensor:
+        """The step of ``_decode_core_modules`` on the fused decode kernels: per layer and
+        loop one q/k/v GEMV with RoPE, the cache readers, one o_proj GEMV (+ the loop-2
+        projection for loops 3/4), one residual/norm chain, one SwiGLU GEMV, one down GEMV
+        and one chain that also applies the next layer's input norm (and the final norm at
+        the end of a loop).  Each op rounds to bf16 where the torch modules do."""
+        cfg = self.config
+        sparse = cfg.enable_sparse_decode
+        fraction = cfg.effective_decode_key_fraction
+        eps = float(self.model.config.rms_norm_eps)
+        layers_w, extra = self._fused_weights()
+        bsz = h.shape[0]
+        nl = len(self.layers)
+        heads, hd = self.layers[0].self_attn.num_heads, self.layers[0].self_attn.head_dim
+        cos, sin = self.backbone.rotary_emb(h, pos_t)
+        rope = (cos.reshape(bsz, hd), sin.reshape(bsz, hd))
+        hid = h.reshape(bsz, -1)
+        _, z = kernels.norm_chain(hid, w_b=layers_w[0]["ln1"], eps=eps, want_h=False)
+        cur_k = [[None] * 4 for _ in range(nl)]
+        cur_v = [[None] * 4 for _ in range(nl)]
+        sources: list[_LayerSource | None] = [None] * nl
+        for loop in range(4):
+            for li, layer in enumerate(self.layers):
+                w = layers_w[li]
+                a = layer.self_attn
+                q, k, v = kernels.gemv(z, [w["q"], w["k"], w["v"]], epilogue=kernels.EPI_ROPE, rope=rope,
+                                       head_dim=hd)
+                q, k, v = (t.view(bsz, heads, 1, hd) for t in (q, k, v))
+                cur_k[li][loop] = k
+                cur_v[li][loop] = v
+                lc = cache.layers[li]
+                if loop < 2 or not sparse:
+                    out, lg = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
+                                                        scaling=a.scaling, return_logits=(loop == 1 and sparse))
+                    projected = kernels.gemv(out.reshape(bsz, -1), [w["o"]])
+                    if loop == 1 and sparse:
+                        idx, valid, mass, sw, _ = lc.select_decode_keys(lg, fraction)
+                        sources[li] = _LayerSource(projected, idx, valid, mass, sw, v)
+                else:
+                    src = sources[li]
+                    if src.selected_output is None:
+                        delta, so = lc.cached_mass_sparse_attention_delta_with_source(
+                            loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
+                            source_weights=src.selected_weights, source_current_value=src.current_value,
+                            global_mass=src.global_mass, scaling=a.scaling)
+                        src.selected_output = so
+                    else:
+                        delta = lc.cached_mass_sparse_attention_delta(
+                            loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
+                            source_selected_output=src.selected_output, global_mass=src.global_mass,
+                            scaling=a.scaling)
+                    projected = kernels.gemv(delta.reshape(bsz, -1), [w["o"]], epilogue=kernels.EPI_ADD,
+                                             addend=src.projected_output)
+                hid, z = kernels.norm_chain(hid, x=projected, w_a=w["ln2"], w_b=w["ln3"], eps=eps)
+                act = kernels.gemv(z, [w["gate"], w["up"]], epilogue=kernels.EPI_SWIGLU)
+                mo = kernels.gemv(act, [w["down"]])
+                last = li == nl - 1
+                nxt = None if (last and loop == 3) else layers_w[(li + 1) % nl]["ln1"]
+                hid, z = kernels.norm_chain(hid, x=mo, w_a=w["ln4"], w_f=extra["norm"] if last else None, w_b=nxt,
+                                            eps=eps)
+        for li in range(nl):
+            cache.layers[li].append_rows(cur_k[li], cur_v[li])
+        return kernels.gemv(hid, [extra["lm_head"]], epilogue=kernels.EPI_F32)
+
+    def _decode_core_modules(self, cache: CrossLoopKVCache, h: torch.Tensor, pos_t: torch.Tensor) -> torch.Tensor:
         """One decode step of ``B`` sequences on the device: every layer and loop, then the
         cache appends (device tail lengths, no host index).  ``h``: embedded tokens
         ``[B, 1, hidden]``; ``pos_t``: their positions ``[B, 1]`` on the device.  Returns

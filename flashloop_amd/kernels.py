@@ -284,3 +284,67 @@ def select_tokens(scores: torch.Tensor, fraction: float, eligible: torch.Tensor 
                                  mask.data_ptr(), pos.data_ptr(), counts.data_ptr(), err.data_ptr(), _stream())
     check(rc, "fl_select_tokens")
     return mask.bool(), pos, counts, err
+
+
+# ---------------------------------------------------------------------------- decode-step model ops
+EPI_PLAIN, EPI_F32, EPI_ADD, EPI_SWIGLU, EPI_ROPE = range(5)
+
+
+def _rows2d(x: torch.Tensor, name: str) -> torch.Tensor:
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"{name} must be bf16 or f32")
+    if not x2.is_cuda:
+        raise RuntimeError(f"{name} must be a device tensor")
+    return x2.contiguous()
+
+
+def gemv(x: torch.Tensor, weights, *, epilogue: int = EPI_PLAIN, addend: torch.Tensor | None = None,
+         rope: tuple[torch.Tensor, torch.Tensor] | None = None, head_dim: int = HEAD_DIM):
+    """``x @ W.T`` for the M <= 8 rows of a decode step (``fl_gemv_bf16``).  ``x``: [..., K]
+    bf16 or f32 (f32 is rounded to bf16 first); ``weights``: list of [N, K] bf16.  Returns
+    [M, N] (bf16, f32 for EPI_F32), or (q, k, v) for EPI_ROPE."""
+    x2 = _rows2d(x, "x")
+    m, k = x2.shape
+    ws = [w if w.is_contiguous() else w.contiguous() for w in weights]
+    for w in ws:
+        _require(w, torch.bfloat16, "weight")
+    n = ws[0].shape[0]
+    dt = torch.float32 if epilogue == EPI_F32 else torch.bfloat16
+    nout = 3 if epilogue == EPI_ROPE else 1
+    outs = [torch.empty(m, n, dtype=dt, device=x2.device) for _ in range(nout)]
+    add = None
+    if epilogue == EPI_ADD:
+        add = addend.reshape(m, n)
+        _require(add, torch.bfloat16, "addend")
+    cos = sin = None
+    if epilogue == EPI_ROPE:
+        cos, sin = (t.reshape(m, head_dim).contiguous() for t in rope)
+        _require(cos, torch.bfloat16, "rope cos")
+        _require(sin, torch.bfloat16, "rope sin")
+    rc = load().fl_gemv_bf16(
+        x2.data_ptr(), int(x2.dtype == torch.float32), k, m, k, C.cast(ptr_array([w.data_ptr() for w in ws]), _lib._PP),
+        n, int(epilogue), C.cast(ptr_array([o.data_ptr() for o in outs]), _lib._PP), n, _p(add), n,
+        _p(cos), _p(sin), int(head_dim), _stream(),
+    )
+    check(rc, "fl_gemv_bf16")
+    return tuple(outs) if epilogue == EPI_ROPE else outs[0]
+
+
+def norm_chain(r: torch.Tensor, *, x: torch.Tensor | None = None, w_a: torch.Tensor | None = None,
+               w_f: torch.Tensor | None = None, w_b: torch.Tensor | None = None, eps: float,
+               want_h: bool = True):
+    """``h = r + RMSNorm_a(x)`` (or ``h = r``), then optionally ``h = RMSNorm_f(h)``, and
+    ``z = RMSNorm_b(h)`` (``fl_norm_chain``).  Returns (h or None, z or None), [M, D] bf16."""
+    r2 = _rows2d(r, "r")
+    m, d = r2.shape
+    x2 = None if x is None else _rows2d(x, "x")
+    for t, nm in ((r2, "r"), (x2, "x")):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError(f"{nm} must be bf16")
+    h = torch.empty(m, d, dtype=torch.bfloat16, device=r2.device) if want_h else None
+    z = torch.empty(m, d, dtype=torch.bfloat16, device=r2.device) if w_b is not None else None
+    rc = load().fl_norm_chain(m, d, float(eps), _p(x2), r2.data_ptr(), _p(w_a), _p(w_f), _p(w_b), _p(h), _p(z), d,
+                              _stream())
+    check(rc, "fl_norm_chain")
+    return h, z

@@ -258,6 +258,36 @@ int32_t fl_select_tokens(const float* scores, int32_t batch, int32_t tokens, dou
                          int32_t* positions, int32_t* counts, int32_t* error_flag,
                          void* stream);
 
+/*
+ * Decode-step model ops -- the per-layer work around the readers in one decode step
+ * (flashloop/engine.py:396-537: q/k/v projections + RoPE, o_proj, the sandwich norms and
+ * residual adds, the SwiGLU MLP, lm_head), fused into few launches.
+ *
+ * fl_gemv_bf16: y[m, n] = sum_k x[m, k] * W[n, k] for m < M (1..8), W bf16 row-major
+ * [N, K] (nn.Linear weights, 16-byte aligned), K % 8 == 0, N % 4 == 0, fp32 accumulation,
+ * output rounded to bf16 as the Linear's.  x is bf16, or f32 (x_is_f32) rounded to bf16
+ * on load (`out.to(bf16)` before o_proj).  epilogue:
+ *   0 plain:  outputs[0] bf16 [M, N]
+ *   1 f32:    outputs[0] f32 [M, N] = the bf16 value widened (lm_head(...).float())
+ *   2 add:    outputs[0] bf16 = bf16(y) + addend (bf16 [M, N], row stride addend_stride)
+ *   3 swiglu: weights = {gate, up}; outputs[0] bf16 = bf16(silu(gate·x)) * (up·x)
+ *   4 rope:   weights = {q, k, v} (each [N, K]); outputs = {q, k, v} bf16 [M, N]; q and k
+ *             get rotate-half RoPE with the bf16 tables rope_cos/rope_sin [M, head_dim]
+ *             (apply_rope, flashloop/engine.py:64-75), each binary op rounded to bf16.
+ * fl_norm_chain: per row m of [M, d] bf16 tensors (row stride `stride`):
+ *   h = x ? r + RMSNorm_a(x) : r;  if w_f: h = RMSNorm_f(h);  h_out = h;  z_out = RMSNorm_b(h)
+ * with RMSNorm_w(v) = bf16(w * v * rsqrt(mean(v^2) + eps)) computed in fp32 (the model's
+ * RMSNorm module); every optional pointer may be NULL.  d <= 8192.
+ */
+int32_t fl_gemv_bf16(const void* x, int32_t x_is_f32, int64_t x_stride, int32_t m, int32_t k,
+                     const uint16_t* const* weights, int32_t n, int32_t epilogue,
+                     void* const* outputs, int64_t out_stride, const uint16_t* addend,
+                     int64_t addend_stride, const uint16_t* rope_cos, const uint16_t* rope_sin,
+                     int32_t head_dim, void* stream);
+int32_t fl_norm_chain(int32_t m, int32_t d, float eps, const uint16_t* x, const uint16_t* r,
+                      const uint16_t* w_a, const uint16_t* w_f, const uint16_t* w_b,
+                      uint16_t* h_out, uint16_t* z_out, int64_t stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
