@@ -76,9 +76,6 @@ class CrossLoopKVLayer:
         self.packed_tokens = torch.zeros(g.batch, dtype=torch.int32, device=dev)
         self.tail_tokens = torch.zeros(g.batch, dtype=torch.int32, device=dev)
         self.late_rows = torch.zeros(2, g.batch, dtype=torch.int32, device=dev)  # rows used in streams 2/3
-        self._row_index = None
-        self._batch_index = None
-        self._one_u8 = torch.ones((), dtype=torch.uint8, device=dev)
         # host mirrors (no device sync on the decode path)
         self.packed_host = [0] * g.batch
         self.tail_host = [0] * g.batch
@@ -315,18 +312,7 @@ class CrossLoopKVLayer:
             raise ValueError("exactly four loop K/V tensors are required")
         if any(t >= self.geometry.tail_capacity for t in self.tail_host):
             raise RuntimeError("tail is full; rollover did not run")
-        b, h = self.batch, self.heads
-        if self._row_index is None:
-            self._row_index = torch.arange(b * h, device=self.device)
-            self._batch_index = torch.arange(b, device=self.device)
-        pos = self.tail_tokens.long()
-        pos_rows = pos.repeat_interleave(h)
-        for r in range(4):
-            self.tail_key[r].index_put_((self._row_index, pos_rows), keys[r].reshape(b * h, HEAD_DIM))
-            self.tail_value[r].index_put_((self._row_index, pos_rows), values[r].reshape(b * h, HEAD_DIM))
-        for s in range(2):
-            self.tail_active[s].index_put_((self._batch_index, pos), self._one_u8)
-        self.tail_tokens += 1
+        kernels.append_tail(self.view(), keys, values, self.tail_active, self.tail_tokens)
 
     def commit_append(self) -> None:
         """Host half of an append: mirrors follow the device lengths; roll full tails."""

@@ -238,10 +238,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------------
-// Residual / RMSNorm chain of one row (one workgroup per row, 256 threads, D <= 8192).
+// Residual / RMSNorm chain of one row (one workgroup per row).  Thread t owns the
+// 8-value chunks t, t + 256, ... of the row; every global load (x, r and the three
+// weight rows) is issued before the first reduction, so the chain costs one memory
+// round trip plus its block reductions.
 // RMSNorm(x) = bf16(w * (x * rsqrt(mean(x^2) + eps))) in fp32, as the model's module.
 constexpr int kNormThreads = 256;
-constexpr int kNormPer = 32;  // values per thread (D <= 8192)
+constexpr int kNormChunks = 4;  // 8-value chunks per thread: D <= 8192
 
 struct NormArgs {
   int D;
@@ -267,49 +270,114 @@ __device__ float norm_block_sum(float v, float* red) {
   return s;
 }
 
-// vals <- RMSNorm(vals) with weight w, rounded to bf16
-__device__ __forceinline__ void rms_apply(float* vals, int n_mine, const uint16_t* w, int D, float eps, float* red) {
+// v <- RMSNorm(v) with weight chunks w (8 values per chunk), rounded to bf16
+template <int NC>
+__device__ __forceinline__ void rms_apply(float (*v)[8], const uint4* w, int nc, int D, float eps, float* red) {
   float ss = 0.0f;
-  for (int i = 0; i < n_mine; ++i) ss = fmaf(vals[i], vals[i], ss);
-  const float ms = norm_block_sum(ss, red) / static_cast<float>(D);
-  const float inv = rsqrtf(ms + eps);
-  for (int i = 0; i < n_mine; ++i) {
-    const int c = threadIdx.x + i * kNormThreads;
-    vals[i] = bf16_round(bf16_to_f32(w[c]) * (vals[i] * inv));
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+    if (i < nc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[i][e], v[i][e], ss);
+  const float inv = rsqrtf(norm_block_sum(ss, red) / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    float wf[8];
+    unpack8(w[i], wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[i][e] = bf16_round(wf[e] * (v[i][e] * inv));
   }
 }
 
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 u;
+  u.x = static_cast<uint32_t>(f32_to_bf16_rne(f[0])) | (static_cast<uint32_t>(f32_to_bf16_rne(f[1])) << 16);
+  u.y = static_cast<uint32_t>(f32_to_bf16_rne(f[2])) | (static_cast<uint32_t>(f32_to_bf16_rne(f[3])) << 16);
+  u.z = static_cast<uint32_t>(f32_to_bf16_rne(f[4])) | (static_cast<uint32_t>(f32_to_bf16_rne(f[5])) << 16);
+  u.w = static_cast<uint32_t>(f32_to_bf16_rne(f[6])) | (static_cast<uint32_t>(f32_to_bf16_rne(f[7])) << 16);
+  return u;
+}
+
+template <int NC>
 __global__ __launch_bounds__(kNormThreads) void norm_chain_kernel(NormArgs a) {
   __shared__ float red[kNormThreads / kWave];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * a.stride;
-  const int n_mine = (a.D - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;
-  float hv[kNormPer];
-  if (a.x != nullptr) {
-    float xv[kNormPer];
+  const int nq = a.D / 8;
+  const int nc = (nq - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;  // my chunks
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  uint4 xr[NC], rr[NC], wa[NC], wf[NC], wb[NC];
 #pragma unroll
-    for (int i = 0; i < kNormPer; ++i)
-      if (i < n_mine) xv[i] = bf16_to_f32(a.x[base + threadIdx.x + i * kNormThreads]);
-    rms_apply(xv, n_mine, a.wa, a.D, a.eps, red);
-#pragma unroll
-    for (int i = 0; i < kNormPer; ++i)
-      if (i < n_mine) hv[i] = bf16_round(bf16_to_f32(a.r[base + threadIdx.x + i * kNormThreads]) + xv[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < kNormPer; ++i)
-      if (i < n_mine) hv[i] = bf16_to_f32(a.r[base + threadIdx.x + i * kNormThreads]);
+  for (int i = 0; i < NC; ++i) {
+    const int q = threadIdx.x + i * kNormThreads;
+    const bool in = i < nc;
+    rr[i] = in ? reinterpret_cast<const uint4*>(a.r + base)[q] : zero;
+    xr[i] = (in && a.x) ? reinterpret_cast<const uint4*>(a.x + base)[q] : zero;
+    wa[i] = (in && a.x) ? reinterpret_cast<const uint4*>(a.wa)[q] : zero;
+    wf[i] = (in && a.wf) ? reinterpret_cast<const uint4*>(a.wf)[q] : zero;
+    wb[i] = (in && a.wb) ? reinterpret_cast<const uint4*>(a.wb)[q] : zero;
   }
-  if (a.wf != nullptr) rms_apply(hv, n_mine, a.wf, a.D, a.eps, red);
+  float h[NC][8];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) unpack8(rr[i], h[i]);
+  if (a.x != nullptr) {
+    float xv[NC][8];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) unpack8(xr[i], xv[i]);
+    rms_apply<NC>(xv, wa, nc, a.D, a.eps, red);
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[i][e] = bf16_round(h[i][e] + xv[i][e]);
+  }
+  if (a.wf != nullptr) rms_apply<NC>(h, wf, nc, a.D, a.eps, red);
   if (a.h_out != nullptr) {
 #pragma unroll
-    for (int i = 0; i < kNormPer; ++i)
-      if (i < n_mine) a.h_out[base + threadIdx.x + i * kNormThreads] = f32_to_bf16_rne(hv[i]);
+    for (int i = 0; i < NC; ++i)
+      if (i < nc) reinterpret_cast<uint4*>(a.h_out + base)[threadIdx.x + i * kNormThreads] = pack8(h[i]);
   }
   if (a.wb != nullptr) {
-    rms_apply(hv, n_mine, a.wb, a.D, a.eps, red);
+    rms_apply<NC>(h, wb, nc, a.D, a.eps, red);
 #pragma unroll
-    for (int i = 0; i < kNormPer; ++i)
-      if (i < n_mine) a.z_out[base + threadIdx.x + i * kNormThreads] = f32_to_bf16_rne(hv[i]);
+    for (int i = 0; i < NC; ++i)
+      if (i < nc) reinterpret_cast<uint4*>(a.z_out + base)[threadIdx.x + i * kNormThreads] = pack8(h[i]);
   }
+}
+
+
+// ---------------------------------------------------------------------------------
+// Decode append: the step's K/V rows of the four loops go to each sequence's tail at its
+// device length, the loop-3/4 activity flags of that row are set, and the length is
+// incremented -- one workgroup per sequence, so the increment follows its own copies.
+constexpr int kAppendThreads = 256;
+
+struct AppendArgs {
+  fl_cache_view v;
+  const uint16_t* k[4];  // [B*H, 128] bf16 rows of the step, per loop
+  const uint16_t* val[4];
+  uint8_t* active[2];  // [B, tail_capacity] loop-3/4 tail activity
+  int32_t* tail_tokens;  // the view's tail lengths, written
+};
+
+__global__ __launch_bounds__(kAppendThreads) void append_tail_kernel(AppendArgs a) {
+  const fl_cache_view& v = a.v;
+  const int b = blockIdx.x;
+  const int pos = v.tail_tokens[b];
+  if (pos < 0 || pos >= v.tail_capacity) return;  // the host rolls over before the tail is full
+  constexpr int kChunks = kDim / 8;              // 16-byte chunks per row
+  const int per = v.heads * kChunks;             // chunks of one tensor for this sequence
+  for (int i = threadIdx.x; i < 8 * per; i += kAppendThreads) {
+    const int t = i / per, rem = i - t * per;
+    const int h = rem / kChunks, c = rem - h * kChunks;
+    const int64_t row = static_cast<int64_t>(b) * v.heads + h;
+    const int loop = t & 3;
+    const uint16_t* src = (t < 4 ? a.k[loop] : a.val[loop]) + row * kDim;
+    uint16_t* dst = static_cast<uint16_t*>(t < 4 ? v.tail_key[loop] : v.tail_value[loop]) +
+                    (row * v.tail_capacity + pos) * kDim;
+    reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(src)[c];
+  }
+  if (threadIdx.x < 2) a.active[threadIdx.x][static_cast<int64_t>(b) * v.tail_capacity + pos] = 1;
+  __syncthreads();
+  if (threadIdx.x == 0) a.tail_tokens[b] = pos + 1;
 }
 
 template <int MT, int EPI>
@@ -394,14 +462,52 @@ extern "C" int32_t fl_norm_chain(int32_t m, int32_t d, float eps, const uint16_t
                                  uint16_t* z_out, int64_t stride, void* stream) {
   using namespace fl;
   clear_error();
-  FL_REQUIRE(m >= 0 && d > 0 && d <= kNormThreads * kNormPer && stride >= d, "fl_norm_chain: bad shape");
+  FL_REQUIRE(m >= 0 && d > 0 && d % 8 == 0 && d <= kNormThreads * kNormChunks * 8 && stride >= d && stride % 8 == 0,
+             "fl_norm_chain: d must be a multiple of 8 up to 8192 and the row stride a multiple of 8");
   FL_REQUIRE(r != nullptr, "fl_norm_chain: null residual/input");
   FL_REQUIRE(x == nullptr || w_a != nullptr, "fl_norm_chain: x needs its norm weight");
   FL_REQUIRE(w_b == nullptr || z_out != nullptr, "fl_norm_chain: z needs an output");
   FL_REQUIRE(h_out != nullptr || z_out != nullptr, "fl_norm_chain: nothing to write");
+  for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(r), static_cast<const void*>(w_a),
+                        static_cast<const void*>(w_f), static_cast<const void*>(w_b),
+                        static_cast<const void*>(h_out), static_cast<const void*>(z_out)})
+    FL_REQUIRE(reinterpret_cast<uintptr_t>(p) % 16 == 0, "fl_norm_chain: every tensor must be 16-byte aligned");
   if (m == 0) return FL_OK;
   NormArgs a{d, eps, x, r, w_a, w_f, w_b, h_out, z_out, stride};
-  hipLaunchKernelGGL(norm_chain_kernel, dim3(m), dim3(kNormThreads), 0, static_cast<hipStream_t>(stream), a);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d <= kNormThreads * 8)
+    hipLaunchKernelGGL(norm_chain_kernel<1>, dim3(m), dim3(kNormThreads), 0, st, a);
+  else if (d <= 2 * kNormThreads * 8)
+    hipLaunchKernelGGL(norm_chain_kernel<2>, dim3(m), dim3(kNormThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(norm_chain_kernel<kNormChunks>, dim3(m), dim3(kNormThreads), 0, st, a);
   FL_LAUNCH_CHECK("fl_norm_chain");
+  return FL_OK;
+}
+
+extern "C" int32_t fl_append_tail(const fl_cache_view* view, const uint16_t* const* keys,
+                                  const uint16_t* const* values, uint8_t* const* tail_active,
+                                  int32_t* tail_tokens, void* stream) {
+  using namespace fl;
+  clear_error();
+  FL_REQUIRE(view && keys && values && tail_active, "fl_append_tail: null argument");
+  const fl_cache_view& v = *view;
+  FL_REQUIRE(v.batch > 0 && v.heads > 0 && v.tail_capacity > 0 && v.tail_tokens, "fl_append_tail: bad view");
+  FL_REQUIRE(tail_tokens == v.tail_tokens, "fl_append_tail: tail_tokens must be the view's length array");
+  AppendArgs a{};
+  a.v = v;
+  for (int r = 0; r < 4; ++r) {
+    FL_REQUIRE(keys[r] && values[r] && v.tail_key[r] && v.tail_value[r], "fl_append_tail: null row or tail");
+    FL_REQUIRE(reinterpret_cast<uintptr_t>(keys[r]) % 16 == 0 && reinterpret_cast<uintptr_t>(values[r]) % 16 == 0,
+               "fl_append_tail: rows must be 16-byte aligned");
+    a.k[r] = keys[r];
+    a.val[r] = values[r];
+  }
+  FL_REQUIRE(tail_active[0] && tail_active[1], "fl_append_tail: null tail_active");
+  a.active[0] = tail_active[0];
+  a.active[1] = tail_active[1];
+  a.tail_tokens = tail_tokens;
+  hipLaunchKernelGGL(append_tail_kernel, dim3(v.batch), dim3(kAppendThreads), 0, static_cast<hipStream_t>(stream), a);
+  FL_LAUNCH_CHECK("fl_append_tail");
   return FL_OK;
 }

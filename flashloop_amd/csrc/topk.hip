@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
 //   4. one prefix scan of the counts, then each lane stores its selected (index, key) at
 //      its offset in an LDS list, which is therefore in index order;
 //   5. the k list entries get their softmax weights and are written out coalesced.
-constexpr int kPer = 35;
+constexpr int kPer = 35;  // most keys per thread (rows of up to kResKeys keys)
 constexpr int kResKeys = kPer * kTopkThreads;
 constexpr int kSelLds = 8 * kTopkThreads;  // selected-list capacity of the resident kernel
 constexpr int kSelPer = kSelLds / kTopkThreads;
@@ -308,10 +308,11 @@ __device__ float res_block_sum(float v, ResShared& sh) {
 
 // Exclusive prefix of sh.cnt in index order (chunk-major, wave-minor), done by wave 0;
 // returns the total.  Caller brackets it with barriers.
+template <int PER>
 __device__ uint32_t prefix_counts(ResShared& sh) {
   if (threadIdx.x < kWave) {
     const int lane = threadIdx.x;
-    constexpr int kN = kPer * kTopkWaves;
+    constexpr int kN = PER * kTopkWaves;
     constexpr int kEach = (kN + kWave - 1) / kWave;
     uint32_t* c = &sh.cnt[0][0];
     uint32_t loc[kEach];
@@ -341,6 +342,7 @@ __device__ uint32_t prefix_counts(ResShared& sh) {
   return sh.total;
 }
 
+template <int PER>
 __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(const float* scores, int64_t stride,
                                                                             const int32_t* n_keys, int rows_per_count,
                                                                             double fraction, int cap, int32_t* indices,
@@ -352,7 +354,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const float* x = scores + static_cast<int64_t>(r) * stride;
   int n = min(n_keys[r / rows_per_count], static_cast<int>(min<int64_t>(stride, 0x7fffffff)));
-  n = min(n, kResKeys);
+  n = min(n, PER * kTopkThreads);
   int32_t* oi = indices + static_cast<int64_t>(r) * cap;
   uint8_t* ov = valid + static_cast<int64_t>(r) * cap;
   float* ow = weights + static_cast<int64_t>(r) * cap;
@@ -382,17 +384,17 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   // padding then adds 0 to the normaliser, lands in bin 0 (whose count is corrected), is
   // never a boundary candidate and never compares above the k-th key, so no later pass
   // needs an index test.
-  uint32_t kr[kPer];
+  uint32_t kr[PER];
   float mx = -INFINITY, mn = INFINITY;
   {
-    float xs[kPer];
+    float xs[PER];
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
+    for (int j = 0; j < PER; ++j) {
       const int i = j * kTopkThreads + tid;
       xs[j] = (i < n) ? x[i] : 0.0f;
     }
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
+    for (int j = 0; j < PER; ++j) {
       const bool in = j * kTopkThreads + tid < n;
       kr[j] = in ? max(order_key(xs[j]), kPadKey + 1u) : kPadKey;
       if (in) {
@@ -415,7 +417,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   float z = 0.0f;
   uint32_t* lin = &sh.hist[0][0];  // one kBins-bin histogram (the sub-histograms are for the radix)
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const float xi = key_value(kr[j]);
     z += fast_exp2(fmaf(xi, kLog2e, -mlog));
     atomicAdd(&lin[value_bin(xi, inv, off)], 1u);
@@ -423,7 +425,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   const float Z = res_block_sum(z, sh);  // (its barriers also complete the histogram)
   {
     const int bin = kBins - 1 - tid;  // descending scan: thread t owns bin kBins-1-t
-    const uint32_t h = lin[bin] - (bin == 0 ? static_cast<uint32_t>(kResKeys - n) : 0u);
+    const uint32_t h = lin[bin] - (bin == 0 ? static_cast<uint32_t>(PER * kTopkThreads - n) : 0u);
     uint32_t incl = h;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -447,7 +449,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   // ---- 3. counts of the keys above B*; keys of B* -> LDS list (one LDS atomic per wave)
   uint32_t cnt_lane = 0;  // lane j: this wave's count of chunk j
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int i = j * kTopkThreads + tid;
     const int b = value_bin(key_value(kr[j]), inv, off);
     const uint64_t bal_a = ballot64(b > bstar);
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
       }
     }
   }
-  if (lane < kPer) sh.cnt[lane][w] = cnt_lane;
+  if (lane < PER) sh.cnt[lane][w] = cnt_lane;
   if (tid < kCand) sh.cand_rank[tid] = 0;
   __syncthreads();
   const int m = static_cast<int>(sh.ncand);
@@ -510,7 +512,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
       for (int i = tid; i < kSubHist * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
       __syncthreads();
 #pragma unroll
-      for (int j = 0; j < kPer; ++j) {
+      for (int j = 0; j < PER; ++j) {
         const uint32_t kk = kr[j];
         if (kk != kPadKey && (kk & pmask) == prefix && value_bin(key_value(kk), inv, off) == bstar)
           atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
@@ -551,15 +553,15 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
     }
     // the `remaining`-th key equal to `prefix` in index order is the k-th key
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
+    for (int j = 0; j < PER; ++j) {
       const bool eq = kr[j] == prefix;
       const uint64_t bal = ballot64(eq);
       if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
     }
     __syncthreads();
-    prefix_counts(sh);
+    prefix_counts<PER>(sh);
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
+    for (int j = 0; j < PER; ++j) {
       const int i = j * kTopkThreads + tid;
       const bool eq = kr[j] == prefix;
       const uint64_t bal = ballot64(eq);
@@ -572,7 +574,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
     __syncthreads();
     const uint32_t kk0 = sh.kth_key, ki0 = sh.kth_idx;
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
+    for (int j = 0; j < PER; ++j) {
       const int i = j * kTopkThreads + tid;
       const uint32_t kk = kr[j];
       const bool sel = kk > kk0 || (kk == kk0 && static_cast<uint32_t>(i) <= ki0);
@@ -583,12 +585,12 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   }
   const uint32_t kth_key = sh.kth_key;
   const uint32_t kth_idx = sh.kth_idx;
-  prefix_counts(sh);  // (its barrier also publishes the counts to every wave)
+  prefix_counts<PER>(sh);  // (its barrier also publishes the counts to every wave)
 
   // ---- 4. selected (index, key) pairs into the LDS list, in index order
-  const uint32_t base_lane = lane < kPer ? sh.cnt[lane][w] : 0u;  // lane j: offset of chunk j
+  const uint32_t base_lane = lane < PER ? sh.cnt[lane][w] : 0u;  // lane j: offset of chunk j
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int i = j * kTopkThreads + tid;
     const uint32_t kk = kr[j];
     const bool sel = kk > kth_key || (kk == kth_key && static_cast<uint32_t>(i) <= kth_idx);
@@ -728,9 +730,19 @@ extern "C" int32_t fl_decode_topk(const float* scores, int64_t scores_stride, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(rows), block(kTopkThreads);  // block: fallback kernel
   // the stride bounds every row's key count: rows that fit in registers take the one-read kernel
-  if (scores_stride <= kResKeys && std::ceil(static_cast<double>(scores_stride) * fraction) <= kSelLds)
-    hipLaunchKernelGGL(decode_topk_resident_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+  // keys per thread: the smallest instantiation that holds the row stride
+  const int per = static_cast<int>((scores_stride + kTopkThreads - 1) / kTopkThreads);
+  if (scores_stride <= kResKeys && std::ceil(static_cast<double>(scores_stride) * fraction) <= kSelLds) {
+    if (per <= 9)
+      hipLaunchKernelGGL(decode_topk_resident_kernel<9>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
                        fraction, capacity, indices, valid, mass, weights, counts);
+    else if (per <= 18)
+      hipLaunchKernelGGL(decode_topk_resident_kernel<18>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+                       fraction, capacity, indices, valid, mass, weights, counts);
+    else
+      hipLaunchKernelGGL(decode_topk_resident_kernel<kPer>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+                       fraction, capacity, indices, valid, mass, weights, counts);
+  }
   else
     hipLaunchKernelGGL(decode_topk_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
                        fraction, capacity, indices, valid, mass, weights, counts);

@@ -348,3 +348,20 @@ def norm_chain(r: torch.Tensor, *, x: torch.Tensor | None = None, w_a: torch.Ten
                               _stream())
     check(rc, "fl_norm_chain")
     return h, z
+
+
+def append_tail(view, keys, values, tail_active, tail_tokens: torch.Tensor) -> None:
+    """Device half of a decode append (``fl_append_tail``): rows ``keys[r]``/``values[r]``
+    ([B, H, 1, 128] bf16, r = loop) to each sequence's tail at its device length."""
+    rows = view.batch * view.heads
+    ks = [_vec(k, rows, "key") for k in keys]
+    vs = [_vec(v, rows, "value") for v in values]
+    for t in tail_active:
+        _require(t, torch.uint8, "tail_active")
+    _require(tail_tokens, torch.int32, "tail_tokens")
+    rc = load().fl_append_tail(
+        C.byref(view), C.cast(ptr_array([k.data_ptr() for k in ks]), _lib._PP),
+        C.cast(ptr_array([v.data_ptr() for v in vs]), _lib._PP),
+        C.cast(ptr_array([t.data_ptr() for t in tail_active]), _lib._PP), tail_tokens.data_ptr(), _stream(),
+    )
+    check(rc, "fl_append_tail")

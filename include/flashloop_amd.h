@@ -277,13 +277,27 @@ int32_t fl_select_tokens(const float* scores, int32_t batch, int32_t tokens, dou
  * fl_norm_chain: per row m of [M, d] bf16 tensors (row stride `stride`):
  *   h = x ? r + RMSNorm_a(x) : r;  if w_f: h = RMSNorm_f(h);  h_out = h;  z_out = RMSNorm_b(h)
  * with RMSNorm_w(v) = bf16(w * v * rsqrt(mean(v^2) + eps)) computed in fp32 (the model's
- * RMSNorm module); every optional pointer may be NULL.  d <= 8192.
+ * RMSNorm module); every optional pointer may be NULL.  d % 8 == 0, d <= 8192, all
+ * tensors 16-byte aligned.
  */
 int32_t fl_gemv_bf16(const void* x, int32_t x_is_f32, int64_t x_stride, int32_t m, int32_t k,
                      const uint16_t* const* weights, int32_t n, int32_t epilogue,
                      void* const* outputs, int64_t out_stride, const uint16_t* addend,
                      int64_t addend_stride, const uint16_t* rope_cos, const uint16_t* rope_sin,
                      int32_t head_dim, void* stream);
+/*
+ * fl_append_tail: the decode append of one layer (CrossLoopKVLayer.append_decode_token,
+ * flashloop/cache.py:1758-1776, device half): for every sequence b, the step's rows
+ * keys[r] / values[r] (bf16 [B*H, 128], r = loop 0..3) are written to tail_key[r] /
+ * tail_value[r] at row tail_tokens[b], tail_active[j][b, tail_tokens[b]] = 1 (u8
+ * [B, tail_capacity], j = loop 3/4), then tail_tokens[b] += 1 (tail_tokens: the view's
+ * length array, passed writable) -- all on the device, so
+ * a captured step replays it.  A sequence whose tail is full is left unchanged (the
+ * caller rolls a group out first).
+ */
+int32_t fl_append_tail(const fl_cache_view* view, const uint16_t* const* keys,
+                       const uint16_t* const* values, uint8_t* const* tail_active,
+                       int32_t* tail_tokens, void* stream);
 int32_t fl_norm_chain(int32_t m, int32_t d, float eps, const uint16_t* x, const uint16_t* r,
                       const uint16_t* w_a, const uint16_t* w_f, const uint16_t* w_b,
                       uint16_t* h_out, uint16_t* z_out, int64_t stride, void* stream);
