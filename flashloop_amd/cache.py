@@ -228,11 +228,11 @@ class CrossLoopKVLayer:
 
     # ------------------------------------------------------------------ readers
     def logits_capacity(self) -> int:
-        """Row stride of the logits buffer: covers the longest prefix plus a full tail and
-        the current token (constant between rollovers, so a captured decode step keeps
-        its buffers), rounded up to 64 floats so that every row starts on a 256-byte
-        boundary."""
-        n = self.quantized_tokens + self.geometry.tail_capacity + 1
+        """Row stride of the logits buffer: the longest possible prefix plus a full tail and
+        the current token (a constant of the layer, so a captured decode step keeps its
+        buffers across rollovers), rounded up to 64 floats so that every row starts on a
+        256-byte boundary."""
+        n = self.geometry.token_capacity + self.geometry.tail_capacity + 1
         return (n + 63) // 64 * 64
 
     def dense_source_attention(self, loop: int, *, query, current_key, current_value, scaling: float,

@@ -719,10 +719,11 @@ int occupancy_of(int loop, bool logits) {
 constexpr int kMaxResident = 2;  // workgroups per CU any reader instantiation can hold
 
 // Persistent grid: every resident 4-wave workgroup slot of the GPU, fewer when the
-// problem is small.
+// cache is small.  Sized from the capacity, not the current lengths, so that the launch
+// (and a graph that captured it) stays valid while the prefixes grow.
 int persist_blocks(const fl_cache_view& v, int occ) {
   const int64_t rows = static_cast<int64_t>(v.batch) * v.heads;
-  const int64_t gmax = rows * (v.max_packed_tokens / kGroup);
+  const int64_t gmax = rows * (v.token_capacity / kGroup);
   const int64_t want = (gmax + rows * kTailUnits + kWaves - 1) / kWaves;
   const int64_t slots = static_cast<int64_t>(cu_count()) * std::min(std::max(occ, 1), kMaxResident);
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(slots, want)));

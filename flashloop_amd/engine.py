@@ -101,8 +101,10 @@ class DecodeRunner:
     """Runs decode steps of one engine's ``_decode_core``: eagerly, or replayed from a HIP
     graph captured per regime (the per-layer launches of a step become one graph
     launch).  The regime is every host value the captured step depends on -- the cache
-    object, the batch, each sequence's packed-prefix length (changes at a rollover), the
-    selection capacity and the logits stride; a change recaptures."""
+    object, the batch, the selection capacity (steps every 64 selected keys) and the
+    logits stride; a change recaptures.  Lengths live on the device and kernel grids are
+    sized from capacities, so a rollover (which rewrites the cache between steps) does
+    not."""
 
     def __init__(self, engine: "FlashLoopEngine", use_graphs: bool) -> None:
         self.engine = engine
@@ -117,7 +119,7 @@ class DecodeRunner:
     def _key(self, cache: CrossLoopKVCache, bsz: int) -> tuple:
         lc = cache.layers[0]
         cap = kernels.decode_capacity(lc.token_count + 1, self.engine.config.effective_decode_key_fraction)
-        return (id(cache), bsz, tuple(lc.packed_host), cap, lc.logits_capacity())
+        return (id(cache), bsz, cap, lc.logits_capacity())
 
     def step(self, cache: CrossLoopKVCache, token_ids: torch.Tensor, positions: Sequence[int]) -> torch.Tensor:
         """Logits ``[B, vocab]`` of one step; the caller then commits the appends
@@ -438,8 +440,8 @@ class FlashLoopEngine:
         """One decode step of ``B`` sequences on the device: every layer and loop, then the
         cache appends (device tail lengths, no host index).  ``h``: embedded tokens
         ``[B, 1, hidden]``; ``pos_t``: their positions ``[B, 1]`` on the device.  Returns
-        the logits ``[B, vocab]``.  Host values it reads (prefix lengths, the selection
-        capacity) change only at a rollover or a capacity step, so it can be captured."""
+        the logits ``[B, vocab]``.  The only host value it reads that changes during decoding
+        is the selection capacity (a step every 64 selected keys), so it can be captured."""
         cfg = self.config
         sparse = cfg.enable_sparse_decode
         fraction = cfg.effective_decode_key_fraction
@@ -505,8 +507,8 @@ class FlashLoopEngine:
     @torch.inference_mode()
     def decode(self, token_ids: torch.Tensor) -> DecodeOutput:
         """``FlashLoopEngine.decode`` (flashloop/engine.py:373-570).  With ``use_graphs`` the
-        step replays a captured HIP graph (recaptured when a rollover or the selection
-        capacity changes its shapes); the returned logits then live in the graph's output
+        step replays a captured HIP graph (recaptured when the selection capacity changes
+        its shapes); the returned logits then live in the graph's output
         buffer and are overwritten by the next step."""
         state = self.state
         if token_ids.shape != (1, 1):

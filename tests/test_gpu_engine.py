@@ -109,8 +109,8 @@ def test_generate_crosses_rollover_and_hooks():
 
 def test_graph_decode_matches_eager():
     """Decode steps replayed from a captured HIP graph equal the eager launches bit for bit,
-    across two rollovers and a change of the selection capacity (which recapture), with
-    the eager rollover packing between replays."""
+    across a rollover (packed eagerly between two replays of the same graph) and a change
+    of the selection capacity (which recaptures)."""
     model = OuroForCausalLM.random_init(TINY, seed=7, device="cuda")
     ids = _ids(700, seed=7)
     eager = FlashLoopEngine(model, use_graphs=False)
@@ -127,7 +127,9 @@ def test_graph_decode_matches_eager():
         captures += graphed._runner.graph is not before
         assert torch.equal(da.logits, db.logits), f"step {i}"
         assert da.receipt == db.receipt
-    assert captures >= 3  # first capture, rollovers at 640 and 704-64, capacity step at 640
+    # the first capture and one at the selection-capacity step (k reaches 64 at 631 keys);
+    # the rollover at step 40 replays the same graph over the repacked cache
+    assert captures == 2
     la, lb = eager.state.cache.layers[0], graphed.state.cache.layers[0]
     assert la.packed_host == lb.packed_host and la.tail_host == lb.tail_host
     for s in range(4):
