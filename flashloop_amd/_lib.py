@@ -43,6 +43,7 @@ class FlCacheView(C.Structure):
         ("tail_tokens", C.c_void_p),
         ("max_packed_tokens", C.c_int32),
         ("max_tail_tokens", C.c_int32),
+        ("value_meta_token", C.c_void_p),
     ]
 
 

@@ -68,6 +68,9 @@ class CrossLoopKVLayer:
         self.value_codes = [c[..., HEAD_DIM // 2 :] for c in self.codes]
         self.key_meta = [torch.zeros(rows, g.token_capacity // GROUP, HEAD_DIM, 2, dtype=torch.float32, device=dev) for _ in range(4)]
         self.value_meta = [torch.zeros(rows, g.row_capacity[s], 2, 2, dtype=torch.float32, device=dev) for s in range(4)]
+        # the V metadata of all four streams again, one 64-byte record per logical token
+        # ([half][stream][scale, min]) for the readers of selected tokens
+        self.value_meta_token = torch.zeros(rows, g.token_capacity, 2, 4, 2, dtype=torch.float32, device=dev)
         self.rank = [torch.full((g.batch, g.token_capacity), -1, dtype=torch.int32, device=dev) for _ in range(2)]
         self.tail_key = [torch.zeros(rows, g.tail_capacity, HEAD_DIM, dtype=torch.bfloat16, device=dev) for _ in range(4)]
         self.tail_value = [torch.zeros(rows, g.tail_capacity, HEAD_DIM, dtype=torch.bfloat16, device=dev) for _ in range(4)]
@@ -123,6 +126,7 @@ class CrossLoopKVLayer:
                 v.tail_key[s] = self.tail_key[s].data_ptr()
                 v.tail_value[s] = self.tail_value[s].data_ptr()
             v.rank[0], v.rank[1] = self.rank[0].data_ptr(), self.rank[1].data_ptr()
+            v.value_meta_token = self.value_meta_token.data_ptr()
             v.packed_tokens = self.packed_tokens.data_ptr()
             v.tail_tokens = self.tail_tokens.data_ptr()
             self._view = v
@@ -375,12 +379,13 @@ class CrossLoopKVLayer:
     #   codes.{s}        u8   [B*H, row_capacity[s], 128]  K codes (bytes 0..63) | V codes (64..127)
     #   key_meta.{s}     f32  [B*H, token_capacity/64, 128, 2]  per-channel (scale, min) per group
     #   value_meta.{s}   f32  [B*H, row_capacity[s], 2, 2]  per-token (scale, min) per 64 channels
+    #   value_meta_token f32  [B*H, token_capacity, 2, 4, 2]  the same per logical token, [half][stream]
     #   rank.{j}         i32  [B, token_capacity]  logical token -> row of stream 2+j, or -1
     #   tail_key.{r}     bf16 [B*H, tail_capacity, 128]  BF16 tail of loop r (tail_value likewise)
     #   tail_active.{j}  u8   [B, tail_capacity]  loop-3/4 activity of the tail rows
     #   packed_tokens / tail_tokens i32 [B], late_rows i32 [2, B]
     FORMAT_NAME = "flashloop_amd.cross_loop_kv"
-    FORMAT_VERSION = 1
+    FORMAT_VERSION = 2
 
     def _named_tensors(self) -> dict[str, torch.Tensor]:
         named = {}
@@ -393,6 +398,7 @@ class CrossLoopKVLayer:
         for j in range(2):
             named[f"rank.{j}"] = self.rank[j]
             named[f"tail_active.{j}"] = self.tail_active[j]
+        named["value_meta_token"] = self.value_meta_token
         named["packed_tokens"] = self.packed_tokens
         named["tail_tokens"] = self.tail_tokens
         named["late_rows"] = self.late_rows
@@ -476,6 +482,7 @@ class CrossLoopKVLayer:
             for s in range(4):
                 tot += h * rows[s] * (64 + 64 + 16)  # K/V codes + V meta
                 tot += h * (p // GROUP) * HEAD_DIM * 8  # K meta
+            tot += h * p * 64  # per-token V metadata records
             tot += 4 * 2 * h * self.tail_host[i] * HEAD_DIM * 2
             tot += 2 * p * 4  # rank maps
         return tot

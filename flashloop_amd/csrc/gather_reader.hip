@@ -308,14 +308,22 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
     const bool bf = t >= Tp;  // BF16 tail row or the current token
     // codes and V metadata of every stream (rows clamped: absent rows read row 0, masked below)
     uint32_t kw[NS][kWords], vw[NS][kWords];
-    float2 vm[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const uint8_t* line = v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + sl.row[s]) * kCodeStride;
       if (kSoftmax) load_words<LPT>(kw[s], line + 4 * kWords * part);
       load_words<LPT>(vw[s], v.value_codes[s] - v.key_codes[s] + line + 4 * kWords * part);
-      vm[s] = *reinterpret_cast<const float2*>(
-          v.value_meta[s] + ((static_cast<int64_t>(bh) * v.row_capacity[s] + sl.row[s]) * 2 + half) * 2);
+    }
+    // V metadata of every stream from the token's 64-byte record (this lane's half: 32 bytes)
+    float2 vm[NS];
+    {
+      const float* rec = v.value_meta_token + ((static_cast<int64_t>(bh) * v.token_capacity + (pre ? t : 0)) * 2 + half) * 8;
+      const float4 r01 = *reinterpret_cast<const float4*>(rec);
+      const float4 r23 = NS > 2 ? *reinterpret_cast<const float4*>(rec + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float2 all[4] = {make_float2(r01.x, r01.y), make_float2(r01.z, r01.w), make_float2(r23.x, r23.y),
+                             make_float2(r23.z, r23.w)};
+#pragma unroll
+      for (int s = 0; s < NS; ++s) vm[s] = all[s];
     }
     // first K-metadata window: groups from the first prefix token's (slots are sorted)
     const uint64_t pre_lanes = kSoftmax ? __ballot(pre) : 0;
@@ -503,7 +511,7 @@ int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t
   FL_REQUIRE(v.packed_tokens && v.tail_tokens, std::string(who) + ": null length arrays");
   FL_REQUIRE(v.tail_key[loop] && v.tail_value[loop], std::string(who) + ": null tail for this loop");
   for (int s = 0; s <= loop && v.max_packed_tokens > 0; ++s) {
-    FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s],
+    FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s] && v.value_meta_token,
                std::string(who) + ": null stream pointer");
     if (s >= 2) FL_REQUIRE(v.rank[s - 2] != nullptr, std::string(who) + ": null rank map");
   }

@@ -220,6 +220,8 @@ __global__ __launch_bounds__(256) void pack_groups_kernel(PackArgs a) {
             make_uint4(words[0], words[1], words[2], words[3]);
         if ((quarter & 1) == 0) {
           *reinterpret_cast<float2*>(v.value_meta[s] + (rowi * 2 + half) * 2) = make_float2(q.scale, q.minimum);
+          const int64_t rec = ((static_cast<int64_t>(bh) * v.token_capacity + t) * 2 + half) * 4 + s;
+          *reinterpret_cast<float2*>(v.value_meta_token + rec * 2) = make_float2(q.scale, q.minimum);
         }
       }
       if (a.rv[r] != nullptr) {
@@ -267,7 +269,7 @@ extern "C" int32_t fl_pack_kv_groups(const fl_cache_view* view, int32_t loops,
   a.loops = loops;
   for (int r = 0; r < loops; ++r) {
     FL_REQUIRE(src_keys[r] && src_values[r], "fl_pack_kv_groups: null source for a loop");
-    FL_REQUIRE(v.key_codes[r] && v.key_meta[r] && v.value_codes[r] && v.value_meta[r],
+    FL_REQUIRE(v.key_codes[r] && v.key_meta[r] && v.value_codes[r] && v.value_meta[r] && v.value_meta_token,
                "fl_pack_kv_groups: destination stream pointer is null");
     FL_REQUIRE(reinterpret_cast<uintptr_t>(src_keys[r]) % 16 == 0 && reinterpret_cast<uintptr_t>(src_values[r]) % 16 == 0,
                "fl_pack_kv_groups: sources must be 16-byte aligned");

@@ -56,6 +56,10 @@ extern "C" {
  *                      logical 64-token group (groups of streams 2/3 are logical too)
  *   value_codes[s] u8  [B*H, row_capacity[s], 64]  row stride FL_CODE_STRIDE
  *   value_meta[s]  f32 [B*H, row_capacity[s], 2, 2]      (scale, min) per 64-channel half
+ *   value_meta_token f32 [B*H, token_capacity, 2, 4, 2]  the same V (scale, min) again,
+ *                      per logical token: [half][stream] in one 64-byte record, so that a
+ *                      reader of selected tokens fetches one line for every stream's
+ *                      V metadata (entries of streams 2/3 at inactive tokens are unused)
  *   rank[0], rank[1] i32 [B, token_capacity]  compact row of stream 2 / 3, or -1
  *   tail_key[r], tail_value[r] bf16 [B*H, tail_capacity, 128]  loop r's BF16 tail
  *   packed_tokens, tail_tokens  i32 [B] (device)  per-sequence prefix / tail lengths
@@ -82,6 +86,7 @@ typedef struct fl_cache_view {
   const int32_t* tail_tokens;
   int32_t max_packed_tokens; /* host-side upper bound of packed_tokens (grid sizing) */
   int32_t max_tail_tokens;   /* host-side upper bound of tail_tokens */
+  float* value_meta_token;   /* per-token V metadata records (written by fl_pack_kv_groups) */
 } fl_cache_view;
 
 /* Message for the last failing call on this thread ("" if none). */

@@ -48,6 +48,23 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == _lib.FL_E_INVALID
 
 
-def test_struct_layout_matches_header():
-    # 4 ints + int[4] + 26 pointers (8 B) + 2 pointers + 2 ints
-    assert C.sizeof(_lib.FlCacheView) == 4 * 4 + 4 * 4 + 26 * 8 + 2 * 8 + 2 * 4
+def test_struct_layout_matches_header(tmp_path):
+    """The ctypes mirror of fl_cache_view has the C struct's size and field offsets
+    (compiled from include/flashloop_amd.h with the host C compiler)."""
+    import shutil
+    import subprocess
+
+    fields = [f[0] for f in _lib.FlCacheView._fields_]
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no host C compiler")
+    inc = Path(__file__).resolve().parents[1] / "include"
+    src = tmp_path / "layout.c"
+    body = "".join(f'  printf("%zu\\n", offsetof(fl_cache_view, {f}));\n' for f in fields)
+    src.write_text("#include <stddef.h>\n#include <stdio.h>\n#include \"flashloop_amd.h\"\n"
+                   "int main(void) {\n" + body + '  printf("%zu\\n", sizeof(fl_cache_view));\n  return 0;\n}\n')
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", str(inc), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    want = [getattr(_lib.FlCacheView, f).offset for f in fields] + [C.sizeof(_lib.FlCacheView)]
+    assert got == want
