@@ -9,8 +9,9 @@ move.  Per (b,h) row, with packed prefix ``Tp``, tail ``tl`` and metadata in flo
   output ``128 * 4``; logits (loop 2) ``(T+1) * 4``;
 * top-k: logits read ``(T+1) * 4`` + indices/valid/weights written ``cap * 9`` + mass;
 * sparse readers: per selected prefix row and stream, K codes 64 + V codes 64 +
-  V metadata 16, plus 1 KiB of K metadata per touched (group, stream); selected tail
-  or current rows 256 per K or V; the selection itself ``cap * 5`` (+ weights 4).
+  V metadata 16, plus 512 B of K metadata per touched (group, stream) -- these readers
+  stream the fp16 copy of the K metadata; selected tail or current rows 256 per K or V;
+  the selection itself ``cap * 5`` (+ weights 4).
 """
 
 from __future__ import annotations
@@ -18,6 +19,7 @@ from __future__ import annotations
 import numpy as np
 
 KMETA_GROUP = 128 * 8  # (scale, min) f32 per channel of one 64-token group
+KMETA_GROUP_F16 = 128 * 4  # the fp16 copy the sparse readers stream
 VMETA_ROW = 2 * 8  # (scale, min) f32 per 64-channel half of one token
 CODE_ROW = 64  # int4 x 128 channels
 BF16_ROW = 256
@@ -78,7 +80,7 @@ def sparse_bytes(stats, cap: int, loop: int, with_source: bool = False) -> int:
         rows_per_stream = [s["prefix"], s["prefix"], s["s2"], s["s3"]][: loop + 1]
         for n in rows_per_stream:
             tot += n * (2 * CODE_ROW + VMETA_ROW)
-        tot += s["groups"] * KMETA_GROUP * (loop + 1)
+        tot += s["groups"] * KMETA_GROUP_F16 * (loop + 1)
         tot += s["other"] * 2 * BF16_ROW
         tot += 3 * BF16_ROW + 128 * 4 + 4 + 128 * 4 + cap * 5
     return tot

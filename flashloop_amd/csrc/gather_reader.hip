@@ -82,7 +82,11 @@ __device__ __forceinline__ float dot_bf16_words(uint4 w, const float* q) {
 //
 // K metadata is per 64-token group: the tile stages q*scale (per channel) and q.min
 // (per part) of W consecutive groups starting at its first prefix token's group in
-// wave-private LDS; tokens beyond the window are handled by further windows.
+// wave-private LDS; tokens beyond the window are handled by further windows.  It is
+// read from the fp16 copy (key_meta_half): with ~6 selected tokens per group, the K
+// metadata is half of these readers' bytes, and fp16 adds less error than the bf16
+// rounding of the reference's residual chain that the fp32 stream sum already departs
+// from.
 // ---------------------------------------------------------------------------------
 template <int LPT>
 struct Lay {
@@ -328,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
     // first K-metadata window: groups from the first prefix token's (slots are sorted)
     const uint64_t pre_lanes = kSoftmax ? __ballot(pre) : 0;
     int gwin = 0;
-    float4 km[kSoftmax ? kWin : 1][NS];
+    uint2 km[kSoftmax ? kWin : 1][NS];  // fp16 (scale, min) of channels 2*lane, 2*lane+1
     if (kSoftmax) {
       const int first = pre_lanes ? __builtin_ctzll(pre_lanes) : 0;
       const int tfirst = __shfl(t, first, kWave);
@@ -337,8 +341,8 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
       for (int j = 0; j < kWin; ++j)
 #pragma unroll
         for (int s = 0; s < NS; ++s)
-          km[j][s] = *reinterpret_cast<const float4*>(
-              v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
+          km[j][s] = *reinterpret_cast<const uint2*>(
+              v.key_meta_half[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
     }
     // next tile's slot (rank rows fly while this tile computes)
     sl = resolve(nxt, ti_n, ok_n, wt_n);
@@ -354,8 +358,8 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
           for (int j = 0; j < kWin; ++j)
 #pragma unroll
             for (int s = 0; s < NS; ++s)
-              km[j][s] = *reinterpret_cast<const float4*>(
-                  v.key_meta[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
+              km[j][s] = *reinterpret_cast<const uint2*>(
+                  v.key_meta_half[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
         }
         const float q0 = L.qf[2 * lane], q1 = L.qf[2 * lane + 1];
         wave_sync_lds();  // earlier reads of the window buffers are done
@@ -363,10 +367,12 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
         for (int j = 0; j < kWin; ++j)
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
-            L.qs[j][s][2 * lane] = q0 * km[j][s].x;
-            L.qs[j][s][2 * lane + 1] = q1 * km[j][s].z * 0.0625f;  // high nibbles read as 16*code
+            const float sc0 = f16_to_f32(km[j][s].x & 0xFFFFu), mn0 = f16_to_f32(km[j][s].x >> 16);
+            const float sc1 = f16_to_f32(km[j][s].y & 0xFFFFu), mn1 = f16_to_f32(km[j][s].y >> 16);
+            L.qs[j][s][2 * lane] = q0 * sc0;
+            L.qs[j][s][2 * lane + 1] = q1 * sc1 * 0.0625f;  // high nibbles read as 16*code
             // q.min over the channels of one part: fold the kCh/2 lanes holding them
-            float m = fmaf(q0, km[j][s].y, q1 * km[j][s].w);
+            float m = fmaf(q0, mn0, q1 * mn1);
             m += dpp<kDppXor1>(m);
             m += dpp<kDppXor2>(m);
             m += dpp<kDppHalfMirror>(m);
@@ -511,7 +517,8 @@ int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t
   FL_REQUIRE(v.packed_tokens && v.tail_tokens, std::string(who) + ": null length arrays");
   FL_REQUIRE(v.tail_key[loop] && v.tail_value[loop], std::string(who) + ": null tail for this loop");
   for (int s = 0; s <= loop && v.max_packed_tokens > 0; ++s) {
-    FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s] && v.value_meta_token,
+    FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s] && v.value_meta_token &&
+                   v.key_meta_half[s],
                std::string(who) + ": null stream pointer");
     if (s >= 2) FL_REQUIRE(v.rank[s - 2] != nullptr, std::string(who) + ": null rank map");
   }

@@ -124,8 +124,12 @@ __global__ __launch_bounds__(256) void pack_groups_kernel(PackArgs a) {
       const Quant q1 = make_quant(mn1, mx1, nact > 0);
       if (quarter == 0) {
         float4 meta = make_float4(q0.scale, q0.minimum, q1.scale, q1.minimum);
-        float* dst = v.key_meta[s] + ((static_cast<int64_t>(bh) * (v.token_capacity / kGroup) + g) * kDim + 2 * pair) * 2;
-        *reinterpret_cast<float4*>(dst) = meta;
+        const int64_t mi = ((static_cast<int64_t>(bh) * (v.token_capacity / kGroup) + g) * kDim + 2 * pair) * 2;
+        *reinterpret_cast<float4*>(v.key_meta[s] + mi) = meta;
+        const uint2 half_meta = make_uint2(
+            static_cast<uint32_t>(f32_to_f16_sat(q0.scale)) | (static_cast<uint32_t>(f32_to_f16_sat(q0.minimum)) << 16),
+            static_cast<uint32_t>(f32_to_f16_sat(q1.scale)) | (static_cast<uint32_t>(f32_to_f16_sat(q1.minimum)) << 16));
+        *reinterpret_cast<uint2*>(v.key_meta_half[s] + mi) = half_meta;
       }
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
@@ -269,7 +273,8 @@ extern "C" int32_t fl_pack_kv_groups(const fl_cache_view* view, int32_t loops,
   a.loops = loops;
   for (int r = 0; r < loops; ++r) {
     FL_REQUIRE(src_keys[r] && src_values[r], "fl_pack_kv_groups: null source for a loop");
-    FL_REQUIRE(v.key_codes[r] && v.key_meta[r] && v.value_codes[r] && v.value_meta[r] && v.value_meta_token,
+    FL_REQUIRE(v.key_codes[r] && v.key_meta[r] && v.value_codes[r] && v.value_meta[r] && v.value_meta_token &&
+                   v.key_meta_half[r],
                "fl_pack_kv_groups: destination stream pointer is null");
     FL_REQUIRE(reinterpret_cast<uintptr_t>(src_keys[r]) % 16 == 0 && reinterpret_cast<uintptr_t>(src_values[r]) % 16 == 0,
                "fl_pack_kv_groups: sources must be 16-byte aligned");
