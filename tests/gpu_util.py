@@ -84,6 +84,7 @@ def flat_rows(x: np.ndarray, lengths=None):
 
 def assert_close(got: np.ndarray, want: np.ndarray, max_abs: float = 2e-2, mean_abs: float = 1e-3, what: str = ""):
     err = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
+    print(f"[parity] {what}: max abs {err.max():.3e} mean abs {err.mean():.3e}", flush=True)
     assert err.max() <= max_abs, f"{what}: max abs err {err.max():.3e} > {max_abs}"
     assert err.mean() <= mean_abs, f"{what}: mean abs err {err.mean():.3e} > {mean_abs}"
     return float(err.max()), float(err.mean())
