@@ -45,6 +45,7 @@ class FlCacheView(C.Structure):
         ("max_tail_tokens", C.c_int32),
         ("value_meta_token", C.c_void_p),
         ("key_meta_half", C.c_void_p * 4),
+        ("value_meta_half", C.c_void_p * 4),
     ]
 
 

@@ -1,10 +1,11 @@
 """Algorithmic (unique, compulsory) HBM bytes of each decode-step kernel.
 
 The roofline numerator: bytes a kernel must move at minimum, not what it happens to
-move.  Per (b,h) row, with packed prefix ``Tp``, tail ``tl`` and metadata in float32:
+move.  Per (b,h) row, with packed prefix ``Tp`` and tail ``tl``; the readers stream the
+fp16 copies of the metadata (the fp32 values are the stored codec state):
 
 * packed stream, dense read: K codes ``Tp*64`` + V codes ``Tp*64``
-  + K (scale,min) ``Tp/64 * 128 * 8`` + V (scale,min) ``Tp * 2 * 8``;
+  + K (scale,min) ``Tp/64 * 128 * 4`` + V (scale,min) ``Tp * 2 * 4``;
 * BF16 tail: ``tl * 128 * 2`` each for K and V; vectors q/k_cur/v_cur ``3 * 256``;
   output ``128 * 4``; logits (loop 2) ``(T+1) * 4``;
 * top-k: logits read ``(T+1) * 4`` + indices/valid/weights written ``cap * 9`` + mass;
@@ -19,7 +20,8 @@ from __future__ import annotations
 import numpy as np
 
 KMETA_GROUP = 128 * 8  # (scale, min) f32 per channel of one 64-token group
-KMETA_GROUP_F16 = 128 * 4  # the fp16 copy the sparse readers stream
+KMETA_GROUP_F16 = 128 * 4  # the fp16 copy the readers stream
+VMETA_ROW_F16 = 2 * 4  # the fp16 copy the dense readers stream
 VMETA_ROW = 2 * 8  # (scale, min) f32 per 64-channel half of one token
 CODE_ROW = 64  # int4 x 128 channels
 BF16_ROW = 256
@@ -29,7 +31,7 @@ def dense_bytes(packed, tail, streams: int, logits: bool) -> int:
     """Sum over rows of one dense reader call; ``packed``/``tail`` per row."""
     p = np.asarray(packed, np.int64)
     t = np.asarray(tail, np.int64)
-    per_stream = p * 2 * CODE_ROW + (p // 64) * KMETA_GROUP + p * VMETA_ROW
+    per_stream = p * 2 * CODE_ROW + (p // 64) * KMETA_GROUP_F16 + p * VMETA_ROW_F16
     tot = streams * per_stream + t * 2 * BF16_ROW + 3 * BF16_ROW + 128 * 4
     if logits:
         tot = tot + (p + t + 1) * 4

@@ -74,6 +74,8 @@ class CrossLoopKVLayer:
         # fp16 copy of the K metadata, streamed by the readers of selected tokens
         self.key_meta_half = [torch.zeros(rows, g.token_capacity // GROUP, HEAD_DIM, 2, dtype=torch.float16, device=dev)
                               for _ in range(4)]
+        self.value_meta_half = [torch.zeros(rows, g.row_capacity[s], 2, 2, dtype=torch.float16, device=dev)
+                                for s in range(4)]
         self.rank = [torch.full((g.batch, g.token_capacity), -1, dtype=torch.int32, device=dev) for _ in range(2)]
         self.tail_key = [torch.zeros(rows, g.tail_capacity, HEAD_DIM, dtype=torch.bfloat16, device=dev) for _ in range(4)]
         self.tail_value = [torch.zeros(rows, g.tail_capacity, HEAD_DIM, dtype=torch.bfloat16, device=dev) for _ in range(4)]
@@ -132,6 +134,7 @@ class CrossLoopKVLayer:
             v.value_meta_token = self.value_meta_token.data_ptr()
             for s in range(4):
                 v.key_meta_half[s] = self.key_meta_half[s].data_ptr()
+                v.value_meta_half[s] = self.value_meta_half[s].data_ptr()
             v.packed_tokens = self.packed_tokens.data_ptr()
             v.tail_tokens = self.tail_tokens.data_ptr()
             self._view = v
@@ -385,13 +388,14 @@ class CrossLoopKVLayer:
     #   key_meta.{s}     f32  [B*H, token_capacity/64, 128, 2]  per-channel (scale, min) per group
     #   value_meta.{s}   f32  [B*H, row_capacity[s], 2, 2]  per-token (scale, min) per 64 channels
     #   value_meta_token f32  [B*H, token_capacity, 2, 4, 2]  the same per logical token, [half][stream]
-    #   key_meta_half.{s} f16 [B*H, token_capacity/64, 128, 2]  key_meta rounded to fp16 (sparse readers)
+    #   key_meta_half.{s} f16 [B*H, token_capacity/64, 128, 2]  key_meta rounded to fp16 (read by the readers)
+    #   value_meta_half.{s} f16 [B*H, row_capacity[s], 2, 2]  value_meta rounded to fp16 (read by the dense readers)
     #   rank.{j}         i32  [B, token_capacity]  logical token -> row of stream 2+j, or -1
     #   tail_key.{r}     bf16 [B*H, tail_capacity, 128]  BF16 tail of loop r (tail_value likewise)
     #   tail_active.{j}  u8   [B, tail_capacity]  loop-3/4 activity of the tail rows
     #   packed_tokens / tail_tokens i32 [B], late_rows i32 [2, B]
     FORMAT_NAME = "flashloop_amd.cross_loop_kv"
-    FORMAT_VERSION = 3
+    FORMAT_VERSION = 4
 
     def _named_tensors(self) -> dict[str, torch.Tensor]:
         named = {}
@@ -400,6 +404,7 @@ class CrossLoopKVLayer:
             named[f"key_meta.{s}"] = self.key_meta[s]
             named[f"value_meta.{s}"] = self.value_meta[s]
             named[f"key_meta_half.{s}"] = self.key_meta_half[s]
+            named[f"value_meta_half.{s}"] = self.value_meta_half[s]
             named[f"tail_key.{s}"] = self.tail_key[s]
             named[f"tail_value.{s}"] = self.tail_value[s]
         for j in range(2):
@@ -487,7 +492,7 @@ class CrossLoopKVLayer:
             p = self.packed_host[i]
             rows = [p, p, self.late_rows_host[0][i], self.late_rows_host[1][i]]
             for s in range(4):
-                tot += h * rows[s] * (64 + 64 + 16)  # K/V codes + V meta
+                tot += h * rows[s] * (64 + 64 + 16 + 8)  # K/V codes + V meta (f32 and f16)
                 tot += h * (p // GROUP) * HEAD_DIM * 8  # K meta
             tot += h * p * 64  # per-token V metadata records
             tot += 4 * h * (p // GROUP) * HEAD_DIM * 4  # fp16 K metadata copies

@@ -183,9 +183,9 @@ struct PrefixLds {
 // channels (rows change along the global sequence).
 template <int NS>
 struct GroupSet {
-  float4 km[NS];
+  uint2 km[NS];  // fp16 (scale, min) of channels 2*lane, 2*lane+1
   uint4 kw[4][NS];
-  float4 vm[NS];
+  uint2 vm[NS];  // fp16 (scale, min) of both 64-channel halves of token `lane`
   uint4 vw[4][NS];
   uint32_t qw;   // bf16 q of channels 2*lane, 2*lane+1
   uint32_t has;  // stream s>=2: bit 5*(s-2)+i row present for tile i, bit 5*(s-2)+4 own token
@@ -221,8 +221,8 @@ __device__ __forceinline__ void load_group(GroupSet<NS>& gs, const DenseArgs& a,
   gs.qw = *reinterpret_cast<const uint32_t*>(a.q + static_cast<int64_t>(bh) * kDim + 2 * lane);
 #pragma unroll
   for (int s = 0; s < NS; ++s)
-    gs.km[s] = *reinterpret_cast<const float4*>(v.key_meta[s] +
-                                                ((static_cast<int64_t>(bh) * gcap + gi) * kDim + 2 * lane) * 2);
+    gs.km[s] = *reinterpret_cast<const uint2*>(v.key_meta_half[s] +
+                                               ((static_cast<int64_t>(bh) * gcap + gi) * kDim + 2 * lane) * 2);
   // K and V halves of each 128-byte code line are requested back to back
 #pragma unroll
   for (int s = 0; s < NS; ++s)
@@ -234,8 +234,8 @@ __device__ __forceinline__ void load_group(GroupSet<NS>& gs, const DenseArgs& a,
     }
 #pragma unroll
   for (int s = 0; s < NS; ++s)
-    gs.vm[s] = *reinterpret_cast<const float4*>(v.value_meta[s] +
-                                                (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][4]) * 4);
+    gs.vm[s] = *reinterpret_cast<const uint2*>(v.value_meta_half[s] +
+                                               (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][4]) * 4);
 }
 
 // Wave-level online-softmax state of the prefix path.  m is wave-uniform; l, mu0/mu1
@@ -271,10 +271,12 @@ __device__ __forceinline__ void compute_group(const GroupSet<NS>& gs, WaveState&
   float ymax = 0.0f;
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    y0[s] = q0 * gs.km[s].x;
-    y1[s] = q1 * gs.km[s].z;
+    const float ks0 = f16_to_f32(gs.km[s].x & 0xFFFFu), km0 = f16_to_f32(gs.km[s].x >> 16);
+    const float ks1 = f16_to_f32(gs.km[s].y & 0xFFFFu), km1 = f16_to_f32(gs.km[s].y >> 16);
+    y0[s] = q0 * ks0;
+    y1[s] = q1 * ks1;
     ymax = fmaxf(ymax, fmaxf(fabsf(y0[s]), fabsf(y1[s])));
-    c[s] = fmaf(q0, gs.km[s].y, q1 * gs.km[s].w);
+    c[s] = fmaf(q0, km0, q1 * km1);
   }
   // streams 0/1 are present for every token: one reduction of their sum
   c[0] = wave_sum(NS > 1 ? c[0] + c[1] : c[0]);
@@ -337,11 +339,13 @@ __device__ __forceinline__ void compute_group(const GroupSet<NS>& gs, WaveState&
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const bool ok = s < 2 || ((gs.has >> (5 * (s - 2) + 4)) & 1u);
-    z0[s] = ok ? p * gs.vm[s].x : 0.0f;
-    z1[s] = ok ? p * gs.vm[s].z : 0.0f;
+    const float vs0 = f16_to_f32(gs.vm[s].x & 0xFFFFu), vm0 = f16_to_f32(gs.vm[s].x >> 16);
+    const float vs1 = f16_to_f32(gs.vm[s].y & 0xFFFFu), vm1 = f16_to_f32(gs.vm[s].y >> 16);
+    z0[s] = ok ? p * vs0 : 0.0f;
+    z1[s] = ok ? p * vs1 : 0.0f;
     if (ok) {
-      st.mu0 = fmaf(p, gs.vm[s].y, st.mu0);
-      st.mu1 = fmaf(p, gs.vm[s].w, st.mu1);
+      st.mu0 = fmaf(p, vm0, st.mu0);
+      st.mu1 = fmaf(p, vm1, st.mu1);
     }
     zmax = fmaxf(zmax, fmaxf(z0[s], z1[s]));
   }
@@ -534,8 +538,10 @@ __device__ __forceinline__ void stage_partial(const WaveState& st, float* part) 
   }
 }
 
+// At most two waves per SIMD: a tighter register budget makes the compiler spill the
+// ping-pong load sets to scratch (measured: the loop-1 reader 126 -> 154 us).
 template <int NS, bool LOGITS>
-__global__ __launch_bounds__(kThreads) void dense_reader_kernel(DenseArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void dense_reader_kernel(DenseArgs a) {
   __shared__ WaveLds<NS> sh[kWaves];
   __shared__ float lgsh[LOGITS ? kWaves : 1][LOGITS ? kStageGroups * kGroup : 1];
   __shared__ float psh[kWaves][kStageSegs][kPartial];
@@ -758,7 +764,7 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   FL_REQUIRE(v.packed_tokens && v.tail_tokens, "fl_decode_attn_dense: null length arrays");
   FL_REQUIRE(v.tail_key[loop] && v.tail_value[loop], "fl_decode_attn_dense: null tail for this loop");
   for (int s = 0; s <= loop && v.max_packed_tokens > 0; ++s) {
-    FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s],
+    FL_REQUIRE(v.key_codes[s] && v.key_meta_half[s] && v.value_codes[s] && v.value_meta_half[s],
                "fl_decode_attn_dense: null stream pointer");
     if (s >= 2) FL_REQUIRE(v.rank[s - 2] != nullptr, "fl_decode_attn_dense: null rank map");
   }

@@ -224,6 +224,8 @@ __global__ __launch_bounds__(256) void pack_groups_kernel(PackArgs a) {
             make_uint4(words[0], words[1], words[2], words[3]);
         if ((quarter & 1) == 0) {
           *reinterpret_cast<float2*>(v.value_meta[s] + (rowi * 2 + half) * 2) = make_float2(q.scale, q.minimum);
+          *reinterpret_cast<uint32_t*>(v.value_meta_half[s] + (rowi * 2 + half) * 2) =
+              static_cast<uint32_t>(f32_to_f16_sat(q.scale)) | (static_cast<uint32_t>(f32_to_f16_sat(q.minimum)) << 16);
           const int64_t rec = ((static_cast<int64_t>(bh) * v.token_capacity + t) * 2 + half) * 4 + s;
           *reinterpret_cast<float2*>(v.value_meta_token + rec * 2) = make_float2(q.scale, q.minimum);
         }
@@ -274,7 +276,7 @@ extern "C" int32_t fl_pack_kv_groups(const fl_cache_view* view, int32_t loops,
   for (int r = 0; r < loops; ++r) {
     FL_REQUIRE(src_keys[r] && src_values[r], "fl_pack_kv_groups: null source for a loop");
     FL_REQUIRE(v.key_codes[r] && v.key_meta[r] && v.value_codes[r] && v.value_meta[r] && v.value_meta_token &&
-                   v.key_meta_half[r],
+                   v.key_meta_half[r] && v.value_meta_half[r],
                "fl_pack_kv_groups: destination stream pointer is null");
     FL_REQUIRE(reinterpret_cast<uintptr_t>(src_keys[r]) % 16 == 0 && reinterpret_cast<uintptr_t>(src_values[r]) % 16 == 0,
                "fl_pack_kv_groups: sources must be 16-byte aligned");

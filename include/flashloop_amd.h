@@ -61,10 +61,12 @@ extern "C" {
  *                      reader of selected tokens fetches one line for every stream's
  *                      V metadata (entries of streams 2/3 at inactive tokens are unused)
  *   key_meta_half[s] f16 [B*H, token_capacity/64, 128, 2]  key_meta[s] rounded to fp16
- *                      (saturating): the K metadata the sparse readers stream (half the
- *                      bytes; the reference's CUDA engine keeps all metadata in fp16,
- *                      flashloop/packing.py:46).  The dense readers and every stored
- *                      fp32 value are unaffected.
+ *                      (saturating)
+ *   value_meta_half[s] f16 [B*H, row_capacity[s], 2, 2]  value_meta[s] rounded likewise
+ *                      The readers stream these fp16 copies (half the metadata bytes;
+ *                      the reference's CUDA engine keeps all metadata in fp16,
+ *                      flashloop/packing.py:46); the fp32 values stay the stored,
+ *                      bit-exact codec state.
  *   rank[0], rank[1] i32 [B, token_capacity]  compact row of stream 2 / 3, or -1
  *   tail_key[r], tail_value[r] bf16 [B*H, tail_capacity, 128]  loop r's BF16 tail
  *   packed_tokens, tail_tokens  i32 [B] (device)  per-sequence prefix / tail lengths
@@ -93,6 +95,7 @@ typedef struct fl_cache_view {
   int32_t max_tail_tokens;   /* host-side upper bound of tail_tokens */
   float* value_meta_token;   /* per-token V metadata records (written by fl_pack_kv_groups) */
   uint16_t* key_meta_half[4]; /* fp16 copies of key_meta (written by fl_pack_kv_groups) */
+  uint16_t* value_meta_half[4]; /* fp16 copies of value_meta (written by fl_pack_kv_groups) */
 } fl_cache_view;
 
 /* Message for the last failing call on this thread ("" if none). */
