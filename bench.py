@@ -31,7 +31,7 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per launch of the dense loop-2 reader (reader + merge kernels), measured with
 # rocprofv3 FETCH_SIZE (x2.0 calibration against a 1 GiB copy) + WRITE_SIZE on MI355X;
 # summary in profiles/decode_step_cfg3.md.
-MEASURED_TRAFFIC = {"cfg3": (1345.4 + 17.5) * 1e6}
+MEASURED_TRAFFIC = {"cfg3": (1211.3 + 1.1 + 17.5 + 0.1) * 1e6}
 CONFIGS = {
     "cfg3": dict(batch=8, heads=16, tokens=32768, seed=3),
     "cfg1": dict(batch=1, heads=16, tokens=8192, seed=1),
