@@ -80,27 +80,31 @@ __device__ __forceinline__ float dot_bf16_words(uint4 w, const float* q) {
 // waves per CU overlap each other's load latencies.  Inside a tile LPT lanes own one
 // slot (lane = LPT*n + part, 128/LPT channels per lane, T = 64/LPT slots).
 //
-// K metadata is per 64-token group: the tile stages q*scale (per channel) and q.min
-// (per part) of W consecutive groups starting at its first prefix token's group in
-// wave-private LDS; tokens beyond the window are handled by further windows.  It is
-// read from the fp16 copy (key_meta_half): with ~6 selected tokens per group, the K
-// metadata is half of these readers' bytes, and fp16 adds less error than the bf16
-// rounding of the reference's residual chain that the fp32 stream sum already departs
-// from.
+// K metadata is per 64-token group.  A wave keeps q*scale (per channel) and q.min (per
+// part) of the last kRing groups it loaded in a wave-private LDS ring; as its tiles walk
+// a row's sorted selection, each tile loads only the groups past those already in the
+// ring (about 1.3 per 8-slot tile at 10% retention, instead of a fixed window), so every
+// group's metadata is fetched about once per row and stream.  Metadata is read from the
+// fp16 copy (key_meta_half): with ~6 selected tokens per group, the K metadata is a large
+// share of these readers' requests, and fp16 adds less error than the bf16 rounding of
+// the reference's residual chain that the fp32 stream sum already departs from.
 // ---------------------------------------------------------------------------------
 template <int LPT>
 struct Lay {
   static constexpr int kTok = kWave / LPT;       // slots per tile
   static constexpr int kCh = kDim / LPT;         // channels per lane
   static constexpr int kWords = kRowBytes / LPT / 4;  // code words per lane
-  static constexpr int kWin = LPT == 4 ? 4 : 2;  // K metadata window (groups)
 };
+constexpr int kRing = 4;  // K-metadata groups a wave keeps (q*scale form) in LDS
+constexpr int kNew = 2;   // groups a tile may add to the ring
 
 template <int NS, int LPT>
 struct TileLds {
-  float qs[Lay<LPT>::kWin][NS][kDim];  // q*scale (odd channels pre-divided by 16)
-  float qm[Lay<LPT>::kWin][NS][LPT];   // q.min per part
-  float qf[kDim];                      // q*scaling of the current row
+  float qs[kRing][NS][kDim];  // q*scale of group g in ring slot g % kRing (odd channels pre-divided by 16)
+  float qm[kRing][NS][LPT];   // q.min per part
+  float qs1[NS][kDim];        // one group for tiles that do not fit the ring
+  float qm1[NS][LPT];
+  float qf[kDim];             // q*scaling of the current row
 };
 
 // Sum over the LPT lanes of a slot.
@@ -181,26 +185,45 @@ __device__ __forceinline__ void load_words(uint32_t* w, const uint8_t* src) {
   }
 }
 
+// Load a T at byte offset `off` (32-bit, unsigned) of a wave-uniform base: compiles to a
+// global load with a scalar base and one 32-bit offset register.
+template <typename T>
+__device__ __forceinline__ T load_at(const void* base, uint32_t off) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + off);
+}
+
 __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// The tile loop is a software pipeline three tiles deep, so that a wave always has the
+// code loads of one tile in flight while it computes another:
+//   iteration j issues the selection record of tile j+3, the rank rows of tile j+2 (from
+//   the record loaded in iteration j-1) and the codes/metadata of tile j+1 (rows from
+//   the rank loads of iteration j-1), then computes tile j.
+// Every load of the steady state is unconditional (absent rows read a clamped row and
+// are masked), so the compiler's in-order wait before tile j's arithmetic counts only
+// the loads issued after tile j's.  The loop is unrolled by two with two register sets
+// (a copy of a set still in flight would wait for its loads).
 template <int NS, int MODE, int LPT>
-__global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gather_reader_kernel(GatherArgs a) {
   using Y = Lay<LPT>;
-  constexpr int kCh = Y::kCh, kWords = Y::kWords, kWin = Y::kWin;
+  constexpr int kCh = Y::kCh, kWords = Y::kWords;
   constexpr bool kSoftmax = MODE != kSelectedPV;
   constexpr bool kSource = MODE == kSparseDeltaFused;
   constexpr int kSets = kSource ? 2 : 1;
+  constexpr int kNR = NS > 2 ? NS - 2 : 1;  // rank maps read (streams 2, 3)
   __shared__ TileLds<NS, LPT> lds[kWaves];
   __shared__ float stage[kWaves][kGatherSegs][kSets][kPartial];
   __shared__ int seg_bh[kWaves][kGatherSegs];
   const fl_cache_view& v = a.v;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, part = lane % LPT, n = lane / LPT;
   const int half = part / (LPT / 2);
-  const int w = blockIdx.x * kWaves + wave;
+  // wave-uniform values live in scalar registers: every load below is a scalar base plus
+  // a 32-bit lane offset
+  const int w = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(wave);
   TileLds<NS, LPT>& L = lds[wave];
   const int rows = v.batch * v.heads;
   const int tpr = a.cap / Y::kTok;  // tiles per row
@@ -232,60 +255,161 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
   }
   __syncthreads();
 
-  // Slot of this lane in a tile: token, stream rows, flags.  The index of tile j+1 is
-  // loaded and its rank rows requested while tile j's codes are in flight and computed.
-  struct Slot {
-    int bh, b, Tp, cur, t;
-    uint32_t has;
-    int row[NS];
+  if (t0 >= t1) {
+    write_stage(0);
+    return;
+  }
+
+  // Tile cursor: row, batch, tile within the row.  Cursors advance one tile at a time (an
+  // integer division per tile would cost ~100 scalar instructions) and stop at the last
+  // tile (tiles past the end are loaded again, never computed).
+  struct Pos {
+    int64_t i;
+    int bh, b, h, k;
+  };
+  auto pos_at = [&](int64_t tile) {
+    Pos p;
+    p.i = tile;
+    p.bh = static_cast<int>(tile / tpr);
+    p.k = static_cast<int>(tile - static_cast<int64_t>(p.bh) * tpr);
+    p.b = p.bh / v.heads;
+    p.h = p.bh - p.b * v.heads;
+    return p;
+  };
+  auto step = [&](Pos& p) {
+    if (p.i + 1 >= t1) return;
+    ++p.i;
+    if (++p.k == tpr) {
+      p.k = 0;
+      ++p.bh;
+      if (++p.h == v.heads) {
+        p.h = 0;
+        ++p.b;
+      }
+    }
+  };
+
+  // ---- stage 1: the selection record of this lane's slot
+  struct Rec {
+    int ti, ok;
     float wt;
   };
-  auto load_idx = [&](int64_t tile, int& ti, int& okv, float& wt) {
-    const int bh = static_cast<int>(tile / tpr);
-    const int64_t sel = static_cast<int64_t>(bh) * a.cap + (tile - static_cast<int64_t>(bh) * tpr) * Y::kTok + n;
-    ti = a.idx[sel];
-    okv = a.valid[sel];
-    wt = (MODE != kSparseDelta) ? a.weights[sel] : 0.0f;
+  auto load_rec = [&](const Pos& p) {
+    const int64_t sel0 = static_cast<int64_t>(p.bh) * a.cap + p.k * Y::kTok;
+    Rec r;
+    r.ti = load_at<int>(a.idx + sel0, 4u * n);
+    r.ok = load_at<uint8_t>(a.valid + sel0, static_cast<uint32_t>(n));
+    r.wt = (MODE != kSparseDelta) ? load_at<float>(a.weights + sel0, 4u * n) : 0.0f;
+    return r;
   };
-  auto resolve = [&](int64_t tile, int ti, int okv, float wt) {
+  // ---- stage 2: the slot (token, lengths) and the raw rank rows of streams 2/3
+  struct Slot {
+    int bh, b, Tp, cur, t;
+    float wt;
+    int rr[kNR];
+  };
+  auto resolve = [&](const Pos& p, const Rec& r) {
     Slot sl;
-    sl.bh = static_cast<int>(tile / tpr);
-    sl.b = sl.bh / v.heads;
+    sl.bh = p.bh;
+    sl.b = p.b;
     sl.Tp = sl.b < kLenCacheG ? len_tp[sl.b] : (min(max(v.packed_tokens[sl.b], 0), v.token_capacity) & ~(kGroup - 1));
     sl.cur = sl.b < kLenCacheG ? len_cur[sl.b] : sl.Tp + min(max(v.tail_tokens[sl.b], 0), v.tail_capacity);
-    sl.t = (okv != 0 && ti >= 0 && ti <= sl.cur) ? ti : -1;  // out-of-range indices are dropped, never read
-    sl.wt = wt;
+    sl.t = (r.ok != 0 && r.ti >= 0 && r.ti <= sl.cur) ? r.ti : -1;  // out-of-range indices are dropped, never read
+    sl.wt = r.wt;
     const bool pre = sl.t >= 0 && sl.t < sl.Tp;
-    sl.has = 0;
+#pragma unroll
+    for (int s = 2; s < NS; ++s)  // unconditional (token 0 for non-prefix slots): masked in stage 3
+      sl.rr[s - 2] = load_at<int>(v.rank[s - 2] + static_cast<int64_t>(sl.b) * v.token_capacity,
+                                  4u * static_cast<uint32_t>(pre ? sl.t : 0));
+    return sl;
+  };
+  // ---- stage 3: codes, V records, new K-metadata groups and query word of a tile
+  struct Tile {
+    int bh, t, Tp, cur;
+    uint32_t has;
+    float wt;
+    int glo, nnew;       // groups glo .. glo+nnew-1 loaded into km (ring additions)
+    int gfirst, glast;   // group span of the tile's prefix slots
+    bool fits;           // every group of the span is in the ring after the additions
+    uint32_t qw;
+    uint32_t kw[NS][kWords], vw[NS][kWords];
+    float4 vm01, vm23;
+    uint2 km[kSoftmax ? kNew : 1][NS];  // fp16 (scale, min) of channels 2*lane, 2*lane+1
+  };
+  // groups already requested for the ring, in issue order (wave-uniform)
+  int ld_bh = -1, ld_hi = -1;
+  auto issue = [&](const Slot& sl) {
+    Tile T;
+    T.bh = sl.bh;
+    T.t = sl.t;
+    T.Tp = sl.Tp;
+    T.cur = sl.cur;
+    T.wt = sl.wt;
+    const bool pre = sl.t >= 0 && sl.t < sl.Tp;
+    T.has = 0;
+    int row[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       int r = pre ? sl.t : -1;
       if (s >= 2 && pre) {
-        r = v.rank[s - 2][static_cast<int64_t>(sl.b) * v.token_capacity + sl.t];
+        r = sl.rr[s - 2];
         if (r >= v.row_capacity[s]) r = -1;
       }
-      if (r >= 0) sl.has |= 1u << s;
-      sl.row[s] = max(r, 0);
+      if (r >= 0) T.has |= 1u << s;
+      row[s] = max(r, 0);
     }
-    return sl;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      // row base (scalar) + line offset (32-bit: row < row_capacity < 2^24)
+      const int64_t base = static_cast<int64_t>(sl.bh) * v.row_capacity[s] * kCodeStride;
+      const uint32_t off = static_cast<uint32_t>(row[s]) * kCodeStride + 4 * kWords * part;
+      if (kSoftmax) load_words<LPT>(T.kw[s], v.key_codes[s] + base + off);
+      load_words<LPT>(T.vw[s], v.value_codes[s] + base + off);
+    }
+    // V metadata of every stream from the token's 64-byte record (this lane's half: 32 bytes)
+    const float* rec = v.value_meta_token + static_cast<int64_t>(sl.bh) * v.token_capacity * 16;
+    const uint32_t roff = static_cast<uint32_t>(pre ? sl.t : 0) * 64u + half * 32u;
+    T.vm01 = load_at<float4>(rec, roff);
+    T.vm23 = NS > 2 ? load_at<float4>(rec, roff + 16u) : make_float4(0.f, 0.f, 0.f, 0.f);
+    T.glo = 0;
+    T.nnew = 0;
+    T.gfirst = 0;
+    T.glast = -1;
+    T.fits = true;
+    if (kSoftmax) {
+      // group span of the prefix slots (slots are sorted) and the groups new to the ring
+      const uint64_t pre_lanes = __ballot(pre);
+      if (pre_lanes) {
+        T.gfirst = __builtin_amdgcn_readfirstlane(__shfl(sl.t, __builtin_ctzll(pre_lanes), kWave)) / kGroup;
+        T.glast = __builtin_amdgcn_readfirstlane(__shfl(sl.t, 63 - __builtin_clzll(pre_lanes), kWave)) / kGroup;
+      }
+      T.glo = sl.bh == ld_bh ? max(T.gfirst, ld_hi + 1) : T.gfirst;
+      const int want = T.glast - T.glo + 1;
+      T.nnew = min(max(want, 0), kNew);
+      T.fits = T.glast - T.gfirst < kRing && want <= kNew;
+      if (T.nnew > 0) {
+        ld_bh = sl.bh;
+        ld_hi = T.glo + T.nnew - 1;
+      }
+#pragma unroll
+      for (int j = 0; j < kNew; ++j)
+        if (j < T.nnew)
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+            T.km[j][s] = load_at<uint2>(v.key_meta_half[s] + (static_cast<int64_t>(sl.bh) * gcap + T.glo + j) * kDim * 2,
+                                        8u * lane);
+      T.qw = load_at<uint32_t>(a.q + static_cast<int64_t>(sl.bh) * kDim, 4u * lane);
+    }
+    return T;
   };
 
   TileOut<LPT, MODE> o;
   tile_reset<LPT, MODE>(o);
   int cur_bh = -1, nseg = 0;
-  if (t0 >= t1) {
-    write_stage(0);
-    return;
-  }
-  int ti_n, ok_n;
-  float wt_n;
-  load_idx(t0, ti_n, ok_n, wt_n);
-  Slot sl = resolve(t0, ti_n, ok_n, wt_n);
 
-  for (int64_t tile = t0; tile < t1; ++tile) {
-    const int64_t nxt = min(tile + 1, t1 - 1);  // the last tile re-reads its own index
-    load_idx(nxt, ti_n, ok_n, wt_n);
-    const int bh = sl.bh;
+  // ---- stage 4: the arithmetic of a tile
+  auto compute = [&](Tile& T) {
+    const int bh = T.bh;
     if (bh != cur_bh) {
       if (cur_bh >= 0) {
         if (nseg == kGatherSegs) {  // stage full: write it out (rare)
@@ -300,107 +424,92 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
       cur_bh = bh;
       if (kSoftmax) {
         wave_sync_lds();
-        const uint32_t qw = *reinterpret_cast<const uint32_t*>(a.q + static_cast<int64_t>(bh) * kDim + 2 * lane);
-        L.qf[2 * lane] = bf16lo_to_f32(qw) * a.scaling;
-        L.qf[2 * lane + 1] = bf16hi_to_f32(qw) * a.scaling;
+        L.qf[2 * lane] = bf16lo_to_f32(T.qw) * a.scaling;
+        L.qf[2 * lane + 1] = bf16hi_to_f32(T.qw) * a.scaling;
       }
     }
-    const int t = sl.t, Tp = sl.Tp, cur = sl.cur;
-    const uint32_t has = sl.has;
-    const float wt = sl.wt;
+    const int t = T.t, Tp = T.Tp, cur = T.cur;
+    const uint32_t has = T.has;
     const bool pre = t >= 0 && t < Tp;
     const bool bf = t >= Tp;  // BF16 tail row or the current token
-    // codes and V metadata of every stream (rows clamped: absent rows read row 0, masked below)
-    uint32_t kw[NS][kWords], vw[NS][kWords];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const uint8_t* line = v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + sl.row[s]) * kCodeStride;
-      if (kSoftmax) load_words<LPT>(kw[s], line + 4 * kWords * part);
-      load_words<LPT>(vw[s], v.value_codes[s] - v.key_codes[s] + line + 4 * kWords * part);
-    }
-    // V metadata of every stream from the token's 64-byte record (this lane's half: 32 bytes)
     float2 vm[NS];
     {
-      const float* rec = v.value_meta_token + ((static_cast<int64_t>(bh) * v.token_capacity + (pre ? t : 0)) * 2 + half) * 8;
-      const float4 r01 = *reinterpret_cast<const float4*>(rec);
-      const float4 r23 = NS > 2 ? *reinterpret_cast<const float4*>(rec + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float2 all[4] = {make_float2(r01.x, r01.y), make_float2(r01.z, r01.w), make_float2(r23.x, r23.y),
-                             make_float2(r23.z, r23.w)};
+      const float2 all[4] = {make_float2(T.vm01.x, T.vm01.y), make_float2(T.vm01.z, T.vm01.w),
+                             make_float2(T.vm23.x, T.vm23.y), make_float2(T.vm23.z, T.vm23.w)};
 #pragma unroll
       for (int s = 0; s < NS; ++s) vm[s] = all[s];
     }
-    // first K-metadata window: groups from the first prefix token's (slots are sorted)
-    const uint64_t pre_lanes = kSoftmax ? __ballot(pre) : 0;
-    int gwin = 0;
-    uint2 km[kSoftmax ? kWin : 1][NS];  // fp16 (scale, min) of channels 2*lane, 2*lane+1
-    if (kSoftmax) {
-      const int first = pre_lanes ? __builtin_ctzll(pre_lanes) : 0;
-      const int tfirst = __shfl(t, first, kWave);
-      gwin = pre_lanes ? tfirst / kGroup : 0;
-#pragma unroll
-      for (int j = 0; j < kWin; ++j)
-#pragma unroll
-        for (int s = 0; s < NS; ++s)
-          km[j][s] = *reinterpret_cast<const uint2*>(
-              v.key_meta_half[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
-    }
-    // next tile's slot (rank rows fly while this tile computes)
-    sl = resolve(nxt, ti_n, ok_n, wt_n);
 
     // ---- logits
     float lg = 0.0f;
     if (kSoftmax) {
       const int gtok = pre ? t / kGroup : -1;
-      float d = 0.0f;
-      for (bool first_win = true;; first_win = false) {  // windows of kWin groups (wave-uniform)
-        if (!first_win) {
+      const float q0 = L.qf[2 * lane], q1 = L.qf[2 * lane + 1];
+      // fp16 (scale, min) of one group and stream -> q*scale (this lane's two channels) and
+      // q.min (folded over the kCh/2 lanes of one part)
+      auto stage_group = [&](uint2 km, float* qs, float* qm) {
+        const float sc0 = f16_to_f32(km.x & 0xFFFFu), mn0 = f16_to_f32(km.x >> 16);
+        const float sc1 = f16_to_f32(km.y & 0xFFFFu), mn1 = f16_to_f32(km.y >> 16);
+        qs[2 * lane] = q0 * sc0;
+        qs[2 * lane + 1] = q1 * sc1 * 0.0625f;  // high nibbles read as 16*code
+        float m = fmaf(q0, mn0, q1 * mn1);
+        m += dpp<kDppXor1>(m);
+        m += dpp<kDppXor2>(m);
+        m += dpp<kDppHalfMirror>(m);
+        if (LPT == 4) m += dpp<kDppMirror>(m);
+        if ((lane & (kCh / 2 - 1)) == 0) qm[lane / (kCh / 2)] = m;
+      };
+      // logit of this lane's slot from the staged q*scale / q.min of its group
+      auto dot_group = [&](const float (*qs)[kDim], const float (*qm)[LPT]) {
+        float d = 0.0f;
 #pragma unroll
-          for (int j = 0; j < kWin; ++j)
+        for (int s = 0; s < NS; ++s) {
+          if (!((has >> s) & 1u)) continue;
+          const float* qq = &qs[s][kCh * part];
+          float e = 0.0f;
 #pragma unroll
-            for (int s = 0; s < NS; ++s)
-              km[j][s] = *reinterpret_cast<const uint2*>(
-                  v.key_meta_half[s] + ((static_cast<int64_t>(bh) * gcap + min(gwin + j, gcap - 1)) * kDim + 2 * lane) * 2);
+          for (int k = 0; k < kWords; ++k) {
+            const float4 x = *reinterpret_cast<const float4*>(qq + 8 * k);
+            const float4 y = *reinterpret_cast<const float4*>(qq + 8 * k + 4);
+            const float qe[4] = {x.x, x.z, y.x, y.z}, qo[4] = {x.y, x.w, y.y, y.w};
+            e = dot8(T.kw[s][k], qe, qo, e);
+          }
+          d += e + qm[s][part];
         }
-        const float q0 = L.qf[2 * lane], q1 = L.qf[2 * lane + 1];
-        wave_sync_lds();  // earlier reads of the window buffers are done
+        return d;
+      };
+      // the tile's new groups -> ring (their loads were issued with the tile)
+      if (T.nnew > 0) {
+        wave_sync_lds();  // earlier reads of the ring slots are done
 #pragma unroll
-        for (int j = 0; j < kWin; ++j)
+        for (int j = 0; j < kNew; ++j)
+          if (j < T.nnew) {
+            const int r = (T.glo + j) & (kRing - 1);
 #pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const float sc0 = f16_to_f32(km[j][s].x & 0xFFFFu), mn0 = f16_to_f32(km[j][s].x >> 16);
-            const float sc1 = f16_to_f32(km[j][s].y & 0xFFFFu), mn1 = f16_to_f32(km[j][s].y >> 16);
-            L.qs[j][s][2 * lane] = q0 * sc0;
-            L.qs[j][s][2 * lane + 1] = q1 * sc1 * 0.0625f;  // high nibbles read as 16*code
-            // q.min over the channels of one part: fold the kCh/2 lanes holding them
-            float m = fmaf(q0, mn0, q1 * mn1);
-            m += dpp<kDppXor1>(m);
-            m += dpp<kDppXor2>(m);
-            m += dpp<kDppHalfMirror>(m);
-            if (LPT == 4) m += dpp<kDppMirror>(m);
-            if ((lane & (kCh / 2 - 1)) == 0) L.qm[j][s][lane / (kCh / 2)] = m;
+            for (int s = 0; s < NS; ++s) stage_group(T.km[j][s], L.qs[r][s], L.qm[r][s]);
           }
         wave_sync_lds();
-        const int js = gtok - gwin;
-        if (pre && js >= 0 && js < kWin) {
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            if (!((has >> s) & 1u)) continue;
-            const float* qq = &L.qs[js][s][kCh * part];
-            float e = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kWords; ++k) {
-              const float4 x = *reinterpret_cast<const float4*>(qq + 8 * k);
-              const float4 y = *reinterpret_cast<const float4*>(qq + 8 * k + 4);
-              const float qe[4] = {x.x, x.z, y.x, y.z}, qo[4] = {x.y, x.w, y.y, y.w};
-              e = dot8(kw[s][k], qe, qo, e);
-            }
-            d += e + L.qm[js][s][part];
-          }
+      }
+      float d = 0.0f;
+      if (T.fits) {
+        if (pre) {
+          const int r = gtok & (kRing - 1);
+          d = dot_group(L.qs[r], L.qm[r]);
         }
-        // tokens past this window: another window
-        const uint64_t rest = __ballot(pre && js >= kWin);
-        if (!rest) break;
-        gwin = __shfl(t, __builtin_ctzll(rest), kWave) / kGroup;
+      } else {
+        // rare: the span exceeds the ring -- one group at a time, loaded on demand
+        for (int g = T.gfirst; g <= T.glast; ++g) {
+          if (!__ballot(pre && gtok == g)) continue;
+          uint2 km1[NS];
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+            km1[s] = load_at<uint2>(v.key_meta_half[s] + (static_cast<int64_t>(bh) * gcap + g) * kDim * 2, 8u * lane);
+          wave_sync_lds();
+#pragma unroll
+          for (int s = 0; s < NS; ++s) stage_group(km1[s], L.qs1[s], L.qm1[s]);
+          wave_sync_lds();
+          if (pre && gtok == g) d = dot_group(L.qs1, L.qm1);
+        }
       }
       // BF16 tail rows and the current token
       if (__ballot(bf)) {
@@ -425,8 +534,8 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
         o.m = tmax;
       }
     }
-    const float p = kSoftmax ? (t >= 0 ? fast_exp2((lg - o.m) * kLog2e) : 0.0f) : (t >= 0 ? wt : 0.0f);
-    const float w1 = kSource ? (t >= 0 ? wt : 0.0f) : 0.0f;
+    const float p = kSoftmax ? (t >= 0 ? fast_exp2((lg - o.m) * kLog2e) : 0.0f) : (t >= 0 ? T.wt : 0.0f);
+    const float w1 = kSource ? (t >= 0 ? T.wt : 0.0f) : 0.0f;
     o.l += p;
 
     // ---- P.V (and the fused loop-2 aggregate sum_S w V_1)
@@ -437,12 +546,12 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
         const float we = p * vm[s].x;
         o.mu = fmaf(p, vm[s].y, o.mu);
 #pragma unroll
-        for (int k = 0; k < kWords; ++k) axpy8(vw[s][k], we, we * 0.0625f, o.acc + 8 * k);
+        for (int k = 0; k < kWords; ++k) axpy8(T.vw[s][k], we, we * 0.0625f, o.acc + 8 * k);
         if (kSource && s < 2) {
           const float ws1 = w1 * vm[s].x;
           o.mu1 = fmaf(w1, vm[s].y, o.mu1);
 #pragma unroll
-          for (int k = 0; k < kWords; ++k) axpy8(vw[s][k], ws1, ws1 * 0.0625f, o.acc1 + 8 * k);
+          for (int k = 0; k < kWords; ++k) axpy8(T.vw[s][k], ws1, ws1 * 0.0625f, o.acc1 + 8 * k);
         }
       }
     }
@@ -462,7 +571,45 @@ __global__ __launch_bounds__(kThreads) void gather_reader_kernel(GatherArgs a) {
         }
       }
     }
+  };
+
+  // ---- prologue: tile t0 issued, rank rows of t0+1 and records of t0+2 in flight.  Each
+  // iteration issues in age order record(j+3), rank(j+2), codes(j+1): a wait for one of
+  // them never waits for younger code loads.
+  Slot s_next;
+  Rec r_next;
+  Tile A, B;
+  Pos pr = pos_at(t0);  // cursor of the next selection record to load
+  Pos ps = pr;          // cursor of the next slot to resolve
+  {
+    const Rec r0 = load_rec(pr);
+    step(pr);
+    const Rec r1 = load_rec(pr);
+    step(pr);
+    r_next = load_rec(pr);
+    const Slot s0 = resolve(ps, r0);
+    step(ps);
+    s_next = resolve(ps, r1);
+    A = issue(s0);
   }
+
+  for (int64_t tile = t0;;) {
+    step(pr);
+    step(ps);
+    Rec r3 = load_rec(pr);           // selection record of tile+3
+    Slot s2 = resolve(ps, r_next);   // rank rows of tile+2
+    B = issue(s_next);               // codes of tile+1
+    compute(A);
+    if (++tile >= t1) break;
+    step(pr);
+    step(ps);
+    r_next = load_rec(pr);
+    s_next = resolve(ps, r3);
+    A = issue(s2);
+    compute(B);
+    if (++tile >= t1) break;
+  }
+
   if (cur_bh >= 0) {
     if (nseg == kGatherSegs) {
       write_stage(nseg);
