@@ -9,8 +9,9 @@ selected aggregate from the rows it reads) and sparse loop 4
 (inputs resident in HBM).  Prints one JSON line.
 
 ``value`` is the step's algorithmic HBM bytes / step time (GB/s); ``roofline`` reports
-the dense loop-2 reader (the dominant kernel) against the 8 TB/s HBM peak, timed with
-HIP events on the launch stream inside the timed steps; ``cpu_baseline`` times the
+the dense loop-2 reader kernel (the dominant kernel) against the 8 TB/s HBM peak, timed
+inside the timed steps with HIP events that the library records on the launch stream
+immediately around that kernel (fl_profile_dense_reader); ``cpu_baseline`` times the
 numpy oracle (a single-core restatement of the reference algorithm) on a bounded
 sample of (b,h) rows of the same workload and scales it to a full step.
 """
@@ -28,10 +29,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "int4 KV-residual decode attn µs/step + HBM GB/s (%peak) at 32K ctx, bs=8"
 HBM_PEAK_GBPS = 8000.0
-# HBM bytes per launch of the dense loop-2 reader (reader + merge kernels), measured with
-# rocprofv3 FETCH_SIZE (x2.0 calibration against a 1 GiB copy) + WRITE_SIZE on MI355X;
-# summary in profiles/decode_step_cfg3.md.
-MEASURED_TRAFFIC = {"cfg3": (1211.3 + 1.1 + 17.5 + 0.1) * 1e6}
+# HBM bytes per launch of the dense loop-2 reader kernel, measured with rocprofv3
+# FETCH_SIZE (x2.0 calibration against a 1 GiB copy) + WRITE_SIZE on MI355X; summary in
+# profiles/decode_step_cfg3.md.
+MEASURED_TRAFFIC = {"cfg3": (1211.3 + 17.5) * 1e6}
 CONFIGS = {
     "cfg3": dict(batch=8, heads=16, tokens=32768, seed=3),
     "cfg1": dict(batch=1, heads=16, tokens=8192, seed=1),
@@ -185,17 +186,17 @@ def main():
     def step():
         return decode_attention_step(layer, queries, kcur, vcur, SCALING, args.fraction)
 
-    # dense loop-2 reader timed alone with events on the launch stream (inside the steps)
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # the dense loop-2 reader kernel is timed by the library: HIP events recorded on the
+    # launch stream around that kernel in each timed step (fl_profile_dense_reader)
+    from flashloop_amd import _lib
+
+    lib = _lib.load()
 
     def timed_step(i):
         out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=kcur[0], current_value=vcur[0],
                                                scaling=SCALING, return_logits=False)
-        ev[i][0].record(stream)
         out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=kcur[1], current_value=vcur[1],
                                                     scaling=SCALING, return_logits=True)
-        ev[i][1].record(stream)
         idx, valid, mass, wts, counts = layer.select_decode_keys(logits, args.fraction)
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
@@ -209,13 +210,21 @@ def main():
         step()
     ref = step()
     torch.cuda.synchronize()
+    _lib.check(lib.fl_profile_dense_reader(1, args.steps), "fl_profile_dense_reader")
     t0 = time.perf_counter()
     for i in range(args.steps):
         timed_step(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_step = elapsed / args.steps * 1e3
-    reader_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+    import ctypes
+
+    tot_ms, n_rec = ctypes.c_float(0.0), ctypes.c_int32(0)
+    _lib.check(lib.fl_profile_dense_reader_read(ctypes.byref(tot_ms), ctypes.byref(n_rec)), "fl_profile_dense_reader_read")
+    _lib.check(lib.fl_profile_dense_reader(1, 0), "fl_profile_dense_reader")
+    if n_rec.value != args.steps:
+        raise RuntimeError(f"expected {args.steps} profiled loop-2 reader launches, got {n_rec.value}")
+    reader_ms = tot_ms.value / n_rec.value
 
     # algorithmic bytes from the actual selection (read back outside the timed region)
     packed = [layer.packed_host[r // H] for r in range(B * H)]
@@ -276,7 +285,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "dense_reader_kernel<2> + merge (loop-2 dense reader)",
+            "kernel": "dense_reader_kernel<2,true> (loop-2 dense reader)",
             "achieved": round(reader_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

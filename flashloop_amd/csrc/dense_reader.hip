@@ -18,6 +18,7 @@
 #include "reader_common.h"
 
 #include <mutex>
+#include <vector>
 
 namespace fl {
 namespace {
@@ -724,6 +725,37 @@ int occupancy_of(int loop, bool logits) {
 
 constexpr int kMaxResident = 2;  // workgroups per CU any reader instantiation can hold
 
+// ---- measurement hook (fl_profile_dense_reader): HIP events around the reader kernel
+struct ReaderProfile {
+  int loop = -1, want = 0, used = 0;
+  bool armed = false;  // the current call records (set by profile_before)
+  std::vector<hipEvent_t> start, stop;
+};
+std::mutex g_prof_mu;
+ReaderProfile g_prof;
+
+void profile_free() {
+  for (hipEvent_t e : g_prof.start) (void)hipEventDestroy(e);
+  for (hipEvent_t e : g_prof.stop) (void)hipEventDestroy(e);
+  g_prof = ReaderProfile{};
+}
+
+void profile_before(hipStream_t st, int loop) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  g_prof.armed = false;
+  if (g_prof.used >= g_prof.want || (g_prof.loop >= 0 && g_prof.loop != loop)) return;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+  if (hipEventRecord(g_prof.start[g_prof.used], st) == hipSuccess) g_prof.armed = true;
+}
+
+void profile_after(hipStream_t st) {
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  if (!g_prof.armed) return;
+  g_prof.armed = false;
+  if (hipEventRecord(g_prof.stop[g_prof.used], st) == hipSuccess) ++g_prof.used;
+}
+
 // Persistent grid: every resident 4-wave workgroup slot of the GPU, fewer when the
 // cache is small.  Sized from the capacity, not the current lengths, so that the launch
 // (and a graph that captured it) stays valid while the prefixes grow.
@@ -737,6 +769,50 @@ int persist_blocks(const fl_cache_view& v, int occ) {
 
 }  // namespace
 }  // namespace fl
+
+extern "C" int32_t fl_profile_dense_reader(int32_t loop, int32_t launches) {
+  using namespace fl;
+  clear_error();
+  FL_REQUIRE(launches >= 0 && launches <= 100000, "fl_profile_dense_reader: launches out of range");
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  profile_free();
+  if (launches == 0) return FL_OK;
+  g_prof.loop = loop;
+  g_prof.want = launches;
+  g_prof.start.resize(launches);
+  g_prof.stop.resize(launches);
+  for (int i = 0; i < launches; ++i) {
+    if (hipEventCreate(&g_prof.start[i]) != hipSuccess || hipEventCreate(&g_prof.stop[i]) != hipSuccess) {
+      g_prof.start.resize(i);
+      g_prof.stop.resize(i);
+      profile_free();
+      set_error("fl_profile_dense_reader: hipEventCreate failed");
+      return FL_E_LAUNCH;
+    }
+  }
+  return FL_OK;
+}
+
+extern "C" int32_t fl_profile_dense_reader_read(float* total_ms, int32_t* launches) {
+  using namespace fl;
+  clear_error();
+  FL_REQUIRE(total_ms && launches, "fl_profile_dense_reader_read: null output");
+  std::lock_guard<std::mutex> g(g_prof_mu);
+  float sum = 0.0f;
+  for (int i = 0; i < g_prof.used; ++i) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(g_prof.stop[i]) != hipSuccess ||
+        hipEventElapsedTime(&ms, g_prof.start[i], g_prof.stop[i]) != hipSuccess) {
+      set_error("fl_profile_dense_reader_read: event query failed");
+      return FL_E_LAUNCH;
+    }
+    sum += ms;
+  }
+  *total_ms = sum;
+  *launches = g_prof.used;
+  g_prof.used = 0;
+  return FL_OK;
+}
 
 extern "C" size_t fl_decode_attn_dense_workspace(const fl_cache_view* view) {
   using namespace fl;
@@ -789,6 +865,7 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   FL_REQUIRE(a.waves + 2 <= kMergeMaxParts, "fl_decode_attn_dense: too many persistent waves for one merge");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(blocks), block(kThreads);
+  profile_before(st, loop);
   const bool lg = logits != nullptr;
   switch (loop * 2 + (lg ? 1 : 0)) {
     case 0: hipLaunchKernelGGL((dense_reader_kernel<1, false>), grid, block, 0, st, a); break;
@@ -800,6 +877,7 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
     case 6: hipLaunchKernelGGL((dense_reader_kernel<4, false>), grid, block, 0, st, a); break;
     default: hipLaunchKernelGGL((dense_reader_kernel<4, true>), grid, block, 0, st, a); break;
   }
+  profile_after(st);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(reader)");
   hipLaunchKernelGGL(dense_merge_kernel, dim3(v.batch * v.heads), dim3(kMergeThreads), 0, st,
                      static_cast<const float*>(a.ws), a.waves, v, out);

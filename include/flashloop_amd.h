@@ -153,6 +153,18 @@ int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Measurement hook (no counterpart in the reference; for benchmarks): record a pair of
+ * HIP events on the launch stream immediately around the reader kernel (not the merge)
+ * of the next `launches` calls of fl_decode_attn_dense with this `loop` index (-1: any).
+ * `launches` = 0 stops recording and frees the events.  Calls made while the stream is
+ * being captured into a graph are not recorded.  fl_profile_dense_reader_read waits
+ * for the recorded events and returns the summed elapsed time and the number of
+ * recorded launches, then clears them.
+ */
+int32_t fl_profile_dense_reader(int32_t loop, int32_t launches);
+int32_t fl_profile_dense_reader_read(float* total_ms, int32_t* launches);
+
+/*
  * J3 -- decode top-k key selection for sparse late-loop decode.
  *
  * Replaces the torch sequence softmax -> topk -> sort -> gather -> `_pad_decode_indices`

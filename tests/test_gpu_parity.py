@@ -344,3 +344,25 @@ def test_hidden_score_and_token_selection():
     m, p, c, err = kernels.select_tokens(flat, 0.1, eligible=el)
     torch.cuda.synchronize()
     assert int(err.item()) == 1
+
+
+def test_profile_hook_records_the_dense_reader():
+    """fl_profile_dense_reader records events around the reader of the selected loop only."""
+    import ctypes
+
+    from flashloop_amd import _lib
+
+    print("case: profile hook", flush=True)
+    w = decode_workload(1, 2, 300, seed=5)
+    layer = _build(w)
+    qs = [w.queries[r].to(DEV) for r in range(4)]
+    cur = [w.current(r) for r in range(4)]
+    lib = _lib.load()
+    _lib.check(lib.fl_profile_dense_reader(1, 3), "fl_profile_dense_reader")
+    for loop in (0, 1, 1):
+        layer.dense_source_attention(loop, query=qs[loop], current_key=cur[loop][0].to(DEV),
+                                     current_value=cur[loop][1].to(DEV), scaling=SCALING, return_logits=loop == 1)
+    tot, n = ctypes.c_float(0.0), ctypes.c_int32(0)
+    _lib.check(lib.fl_profile_dense_reader_read(ctypes.byref(tot), ctypes.byref(n)), "read")
+    _lib.check(lib.fl_profile_dense_reader(1, 0), "stop")
+    assert n.value == 2 and tot.value > 0.0
