@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=8, help="(b,h) rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--eager", action="store_true", help="cfg4: eager decode launches instead of HIP-graph replay")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="cfg4: residual/norm chains as launches of their own, not inside the next GEMV")
     ap.add_argument("--fraction", type=float, default=0.10)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (a known-size kernel that "
@@ -100,6 +102,7 @@ def bench_cfg4(args):
     print(f"[bench] cfg4: random-init model on {torch.cuda.get_device_name(0)}", file=sys.stderr, flush=True)
     eng = FlashLoopEngine.from_random_init(OuroConfig(), seed=cfg["seed"], device=dev)
     eng.use_graphs = not args.eager
+    eng.fused_chain = not args.no_chain
     g = torch.Generator().manual_seed(cfg["seed"])
     ids = torch.randint(0, eng.model.config.vocab_size, (1, cfg["prompt"]), generator=g).to(dev)
     new = cfg["new_tokens"] if args.steps == 50 else max(2, args.steps)
@@ -131,6 +134,7 @@ def bench_cfg4(args):
         "dtype": "bf16 weights / int4 KV",
         "data": "synthetic (random weights, random token ids)",
         "decode_graphs": eng.use_graphs,
+        "fused_chain": eng.fused_chain,
         "prefill_receipts": receipts,
         "config": {"workload": "cfg4", "prompt": cfg["prompt"], "layers": eng.model.config.num_hidden_layers,
                    "hidden": eng.model.config.hidden_size},

@@ -84,6 +84,8 @@ SIGNATURES = {
     "fl_select_tokens": (_I32, [_P, _I32, _I32, _F64, _P, _I32, _P, _P, _P, _P, _P]),
     "fl_gemv_bf16": (_I32, [_P, _I32, _I64, _I32, _I32, _PP, _I32, _I32, _PP, _I64, _P, _I64, _P, _P, _I32, _P]),
     "fl_norm_chain": (_I32, [_I32, _I32, _F32, _P, _P, _P, _P, _P, _P, _P, _I64, _P]),
+    "fl_gemv_bf16_chain": (_I32, [_I32, _I32, _F32, _P, _P, _P, _P, _P, _P, _I64, _PP, _I32, _I32, _PP, _I64, _P,
+                                  _I64, _P, _P, _I32, _P]),
     "fl_append_tail": (_I32, [_VIEW, _PP, _PP, _PP, _P, _P]),
 }
 

@@ -111,68 +111,11 @@ __device__ __forceinline__ void block_rows(const GemvArgs& a, int g, const uint1
   }
 }
 
-template <int MT, int EPI, bool XF32>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
-  __shared__ float red[kGemvWaves][MT][kRows];
+// Cross-wave reduction of the partial dots and the epilogue (wave 0, lane m writes row m).
+template <int MT, int EPI>
+__device__ __forceinline__ void gemv_finish(const GemvArgs& a, float (*acc)[kRows], float (*red)[MT][kRows], int mat,
+                                            int n0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint16_t* rp[kRows];
-  int mat, n0;
-  block_rows<EPI>(a, blockIdx.x, rp, &mat, &n0);
-  float acc[MT][kRows];
-#pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) acc[m][r] = 0.0f;
-  const int nq = a.K / 8;  // 16-byte chunks per row
-  // chunk q = j*256 + wave*64 + lane: each wave reads 1 KB contiguous per row and step
-  constexpr int kStep = kGemvWaves * kWave;
-  int q = wave * kWave + lane;
-  // two steps per iteration keep 8 row loads in flight per lane
-  for (; q + kStep < nq; q += 2 * kStep) {
-    uint4 w0[kRows], w1[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-      w0[r] = reinterpret_cast<const uint4*>(rp[r])[q];
-      w1[r] = reinterpret_cast<const uint4*>(rp[r])[q + kStep];
-    }
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m < a.M) {
-        float x0[8], x1[8];
-        load_x8<XF32>(a, m, q, x0);
-        load_x8<XF32>(a, m, q + kStep, x1);
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-          float f[8];
-          unpack8(w0[r], f);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x0[e], f[e], acc[m][r]);
-          unpack8(w1[r], f);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x1[e], f[e], acc[m][r]);
-        }
-      }
-    }
-  }
-  if (q < nq) {
-    uint4 w0[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) w0[r] = reinterpret_cast<const uint4*>(rp[r])[q];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m < a.M) {
-        float x0[8];
-        load_x8<XF32>(a, m, q, x0);
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-          float f[8];
-          unpack8(w0[r], f);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x0[e], f[e], acc[m][r]);
-        }
-      }
-    }
-  }
 #pragma unroll
   for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -237,6 +180,71 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   }
 }
 
+template <int MT, int EPI, bool XF32>
+__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
+  __shared__ float red[kGemvWaves][MT][kRows];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint16_t* rp[kRows];
+  int mat, n0;
+  block_rows<EPI>(a, blockIdx.x, rp, &mat, &n0);
+  float acc[MT][kRows];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) acc[m][r] = 0.0f;
+  const int nq = a.K / 8;  // 16-byte chunks per row
+  // chunk q = j*256 + wave*64 + lane: each wave reads 1 KB contiguous per row and step
+  constexpr int kStep = kGemvWaves * kWave;
+  int q = wave * kWave + lane;
+  // two steps per iteration keep 8 row loads in flight per lane
+  for (; q + kStep < nq; q += 2 * kStep) {
+    uint4 w0[kRows], w1[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+      w0[r] = reinterpret_cast<const uint4*>(rp[r])[q];
+      w1[r] = reinterpret_cast<const uint4*>(rp[r])[q + kStep];
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < a.M) {
+        float x0[8], x1[8];
+        load_x8<XF32>(a, m, q, x0);
+        load_x8<XF32>(a, m, q + kStep, x1);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+          float f[8];
+          unpack8(w0[r], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x0[e], f[e], acc[m][r]);
+          unpack8(w1[r], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x1[e], f[e], acc[m][r]);
+        }
+      }
+    }
+  }
+  if (q < nq) {
+    uint4 w0[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) w0[r] = reinterpret_cast<const uint4*>(rp[r])[q];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m < a.M) {
+        float x0[8];
+        load_x8<XF32>(a, m, q, x0);
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+          float f[8];
+          unpack8(w0[r], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x0[e], f[e], acc[m][r]);
+        }
+      }
+    }
+  }
+  gemv_finish<MT, EPI>(a, acc, red, mat, n0);
+}
+
 // ---------------------------------------------------------------------------------
 // Residual / RMSNorm chain of one row (one workgroup per row).  Thread t owns the
 // 8-value chunks t, t + 256, ... of the row; every global load (x, r and the three
@@ -259,7 +267,7 @@ struct NormArgs {
   int64_t stride;      // row stride of every [M, D] tensor
 };
 
-__device__ float norm_block_sum(float v, float* red) {
+__device__ __forceinline__ float norm_block_sum(float v, float* red) {
   v = wave_sum(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
@@ -298,51 +306,154 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return u;
 }
 
+// The chain of row `base` (element offset): h = r (+ n_a(x)), optionally h = n_f(h),
+// written to h_out when write_h; then z = n_b(h) when n_b is given.  chain_load issues the
+// loads of this thread's chunks t, t + 256, ...; chain_finish leaves z (or h without n_b)
+// in v as bf16 values.  All kNormThreads threads must call chain_finish (block reductions).
+// A raw buffer resource over `bytes` bytes at p (wave-uniform): loads past the end (or
+// from a resource of size 0) return zero.  Word 3 is the gfx9 raw-buffer format.
+using BufRes = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ BufRes buf_res(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(BufRes r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+}
+
 template <int NC>
-__global__ __launch_bounds__(kNormThreads) void norm_chain_kernel(NormArgs a) {
-  __shared__ float red[kNormThreads / kWave];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * a.stride;
+struct ChainIn {
+  uint4 xr[NC], rr[NC], wa[NC], wf[NC], wb[NC];
+};
+
+template <int NC>
+__device__ __forceinline__ void chain_load(const NormArgs& a, int64_t base, ChainIn<NC>& in) {
   const int nq = a.D / 8;
   const int nc = (nq - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;  // my chunks
-  const uint4 zero = make_uint4(0, 0, 0, 0);
-  uint4 xr[NC], rr[NC], wa[NC], wf[NC], wb[NC];
+  // Buffer loads sized to each operand (size 0 when absent): chunks past the row read as
+  // zero without a branch.  A load under a branch would make the compiler's wait at the
+  // join drain every outstanding load, including a caller's loads issued after these.
+  (void)nc;
+  const uint32_t row = static_cast<uint32_t>(a.D) * 2u;
+  const BufRes r = buf_res(a.r + base, row);
+  const BufRes x = buf_res(a.x ? a.x + base : nullptr, a.x ? row : 0u);
+  const BufRes wa = buf_res(a.x ? a.wa : nullptr, a.x ? row : 0u);
+  const BufRes wf = buf_res(a.wf, a.wf ? row : 0u);
+  const BufRes wb = buf_res(a.wb, a.wb ? row : 0u);
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const int q = threadIdx.x + i * kNormThreads;
-    const bool in = i < nc;
-    rr[i] = in ? reinterpret_cast<const uint4*>(a.r + base)[q] : zero;
-    xr[i] = (in && a.x) ? reinterpret_cast<const uint4*>(a.x + base)[q] : zero;
-    wa[i] = (in && a.x) ? reinterpret_cast<const uint4*>(a.wa)[q] : zero;
-    wf[i] = (in && a.wf) ? reinterpret_cast<const uint4*>(a.wf)[q] : zero;
-    wb[i] = (in && a.wb) ? reinterpret_cast<const uint4*>(a.wb)[q] : zero;
+    const uint32_t off = 16u * static_cast<uint32_t>(threadIdx.x + i * kNormThreads);
+    in.rr[i] = buf_load16(r, off);
+    in.xr[i] = buf_load16(x, off);
+    in.wa[i] = buf_load16(wa, off);
+    in.wf[i] = buf_load16(wf, off);
+    in.wb[i] = buf_load16(wb, off);
   }
-  float h[NC][8];
+}
+
+template <int NC>
+__device__ __forceinline__ void chain_finish(const NormArgs& a, int64_t base, bool write_h, const ChainIn<NC>& in,
+                                             float (*h)[8], float* red) {
+  const int nc = (a.D / 8 - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;
 #pragma unroll
-  for (int i = 0; i < NC; ++i) unpack8(rr[i], h[i]);
+  for (int i = 0; i < NC; ++i) unpack8(in.rr[i], h[i]);
   if (a.x != nullptr) {
     float xv[NC][8];
 #pragma unroll
-    for (int i = 0; i < NC; ++i) unpack8(xr[i], xv[i]);
-    rms_apply<NC>(xv, wa, nc, a.D, a.eps, red);
+    for (int i = 0; i < NC; ++i) unpack8(in.xr[i], xv[i]);
+    rms_apply<NC>(xv, in.wa, nc, a.D, a.eps, red);
 #pragma unroll
     for (int i = 0; i < NC; ++i)
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[i][e] = bf16_round(h[i][e] + xv[i][e]);
   }
-  if (a.wf != nullptr) rms_apply<NC>(h, wf, nc, a.D, a.eps, red);
-  if (a.h_out != nullptr) {
+  if (a.wf != nullptr) rms_apply<NC>(h, in.wf, nc, a.D, a.eps, red);
+  if (write_h && a.h_out != nullptr) {
 #pragma unroll
     for (int i = 0; i < NC; ++i)
       if (i < nc) reinterpret_cast<uint4*>(a.h_out + base)[threadIdx.x + i * kNormThreads] = pack8(h[i]);
   }
+  if (a.wb != nullptr) rms_apply<NC>(h, in.wb, nc, a.D, a.eps, red);
+}
+
+template <int NC>
+__device__ __forceinline__ void chain_row(const NormArgs& a, int64_t base, bool write_h, float (*h)[8], float* red) {
+  ChainIn<NC> in;
+  chain_load<NC>(a, base, in);
+  chain_finish<NC>(a, base, write_h, in, h, red);
+}
+
+template <int NC>
+__global__ __launch_bounds__(kNormThreads) void norm_chain_kernel(NormArgs a) {
+  __shared__ float red[kNormThreads / kWave];
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * a.stride;
+  const int nc = (a.D / 8 - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;
+  float h[NC][8];
+  chain_row<NC>(a, base, true, h, red);
   if (a.wb != nullptr) {
-    rms_apply<NC>(h, wb, nc, a.D, a.eps, red);
 #pragma unroll
     for (int i = 0; i < NC; ++i)
       if (i < nc) reinterpret_cast<uint4*>(a.z_out + base)[threadIdx.x + i * kNormThreads] = pack8(h[i]);
   }
 }
 
+// GEMV whose input rows are the chain's output, computed in the prologue of every
+// workgroup (bit-identical to norm_chain_kernel: same chunk ownership, same reductions);
+// workgroup 0 writes h.  The weight chunks are requested before the chain so its loads
+// and reductions run under their latency.  K <= kChainMaxK (each thread's x chunks are the
+// chunks it normalises, so z stays in registers).
+constexpr int kChainSteps = 2;
+constexpr int kChainMaxK = kChainSteps * kGemvThreads * 8;
+static_assert(kGemvThreads == kNormThreads, "the chain prologue maps one GEMV thread to one chain thread");
+
+template <int MT, int EPI, int NC>
+__global__ __launch_bounds__(kGemvThreads) void gemv_chain_kernel(GemvArgs a, NormArgs c) {
+  __shared__ float red[kGemvWaves][MT][kRows];
+  __shared__ float nred[kNormThreads / kWave];
+  const uint16_t* rp[kRows];
+  int mat, n0;
+  block_rows<EPI>(a, blockIdx.x, rp, &mat, &n0);
+  const int nq = a.K / 8;
+  constexpr int kStep = kGemvThreads;
+  const int q = threadIdx.x;
+  // row 0's chain inputs are requested before the weights: the wave's loads return in
+  // order, so the chain (two block reductions) then runs while the weights are in flight
+  ChainIn<NC> in0;
+  chain_load<NC>(c, 0, in0);
+  __builtin_amdgcn_sched_barrier(0);  // keep the issue order: chain inputs, then weights
+  uint4 wv[NC][kRows];  // weight chunks past K (buffer bounds) read as zero, no branch
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const BufRes wr = buf_res(rp[r], static_cast<uint32_t>(a.K) * 2u);
+#pragma unroll
+    for (int s = 0; s < NC; ++s) wv[s][r] = buf_load16(wr, 16u * static_cast<uint32_t>(q + s * kStep));
+  }
+  float acc[MT][kRows];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) acc[m][r] = 0.0f;
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    if (m < a.M) {
+      float z[NC][8];
+      if (m == 0)
+        chain_finish<NC>(c, 0, blockIdx.x == 0, in0, z, nred);
+      else
+        chain_row<NC>(c, static_cast<int64_t>(m) * c.stride, blockIdx.x == 0, z, nred);
+#pragma unroll
+      for (int s = 0; s < NC; ++s)
+        if (q + s * kStep < nq)
+#pragma unroll
+          for (int r = 0; r < kRows; ++r) {
+            float f[8];
+            unpack8(wv[s][r], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(z[s][e], f[e], acc[m][r]);
+          }
+    }
+  }
+  gemv_finish<MT, EPI>(a, acc, red, mat, n0);
+}
 
 // ---------------------------------------------------------------------------------
 // Decode append: the step's K/V rows of the four loops go to each sequence's tail at its
@@ -400,39 +511,55 @@ void launch_gemv(const GemvArgs& a, int blocks, hipStream_t st) {
     launch_gemv_m<8, EPI>(a, blocks, st);
 }
 
-}  // namespace
-}  // namespace fl
+template <int EPI, int NC>
+void launch_gemv_chain_nc(const GemvArgs& a, const NormArgs& c, int blocks, hipStream_t st) {
+  if (a.M <= 1)
+    hipLaunchKernelGGL((gemv_chain_kernel<1, EPI, NC>), dim3(blocks), dim3(kGemvThreads), 0, st, a, c);
+  else if (a.M <= 2)
+    hipLaunchKernelGGL((gemv_chain_kernel<2, EPI, NC>), dim3(blocks), dim3(kGemvThreads), 0, st, a, c);
+  else if (a.M <= 4)
+    hipLaunchKernelGGL((gemv_chain_kernel<4, EPI, NC>), dim3(blocks), dim3(kGemvThreads), 0, st, a, c);
+  else
+    hipLaunchKernelGGL((gemv_chain_kernel<8, EPI, NC>), dim3(blocks), dim3(kGemvThreads), 0, st, a, c);
+}
 
-extern "C" int32_t fl_gemv_bf16(const void* x, int32_t x_is_f32, int64_t x_stride, int32_t m, int32_t k,
-                                const uint16_t* const* weights, int32_t n, int32_t epilogue, void* const* outputs,
-                                int64_t out_stride, const uint16_t* addend, int64_t addend_stride,
-                                const uint16_t* rope_cos, const uint16_t* rope_sin, int32_t head_dim, void* stream) {
-  using namespace fl;
-  clear_error();
-  FL_REQUIRE(x && weights && outputs, "fl_gemv_bf16: null x/weights/outputs");
-  FL_REQUIRE(m >= 1 && m <= kMaxM, "fl_gemv_bf16: rows of x must be 1..8");
-  FL_REQUIRE(k > 0 && k % 8 == 0 && n > 0 && n % kRows == 0, "fl_gemv_bf16: K must be a multiple of 8, N of 4");
-  FL_REQUIRE(x_stride >= k && out_stride >= n, "fl_gemv_bf16: bad row strides");
+template <int EPI>
+void launch_gemv_chain(const GemvArgs& a, const NormArgs& c, int blocks, hipStream_t st) {
+  if (a.K <= kGemvThreads * 8)
+    launch_gemv_chain_nc<EPI, 1>(a, c, blocks, st);
+  else
+    launch_gemv_chain_nc<EPI, kChainSteps>(a, c, blocks, st);
+}
+
+// Argument checks and GemvArgs shared by both GEMV entry points.
+int32_t make_gemv_args(GemvArgs& a, const void* x, int32_t x_is_f32, int64_t x_stride, int32_t m, int32_t k,
+                       const uint16_t* const* weights, int32_t n, int32_t epilogue, void* const* outputs,
+                       int64_t out_stride, const uint16_t* addend, int64_t addend_stride, const uint16_t* rope_cos,
+                       const uint16_t* rope_sin, int32_t head_dim, const char* who) {
+  const std::string w(who);
+  FL_REQUIRE(x && weights && outputs, w + ": null x/weights/outputs");
+  FL_REQUIRE(m >= 1 && m <= kMaxM, w + ": rows of x must be 1..8");
+  FL_REQUIRE(k > 0 && k % 8 == 0 && n > 0 && n % kRows == 0, w + ": K must be a multiple of 8, N of 4");
+  FL_REQUIRE(x_stride >= k && out_stride >= n, w + ": bad row strides");
   FL_REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && (x_stride * (x_is_f32 ? 4 : 2)) % 16 == 0,
-             "fl_gemv_bf16: x rows must be 16-byte aligned");
-  FL_REQUIRE(epilogue >= kEpiPlain && epilogue <= kEpiRope, "fl_gemv_bf16: unknown epilogue");
+             w + ": x rows must be 16-byte aligned");
+  FL_REQUIRE(epilogue >= kEpiPlain && epilogue <= kEpiRope, w + ": unknown epilogue");
   const int nmat = epilogue == kEpiRope ? 3 : (epilogue == kEpiSwiGlu ? 2 : 1);
-  GemvArgs a{};
   for (int i = 0; i < nmat; ++i) {
     FL_REQUIRE(weights[i] != nullptr && reinterpret_cast<uintptr_t>(weights[i]) % 16 == 0,
-               "fl_gemv_bf16: weights must be non-null and 16-byte aligned");
+               w + ": weights must be non-null and 16-byte aligned");
     a.w[i] = weights[i];
   }
   const int nout = epilogue == kEpiRope ? 3 : 1;
   for (int i = 0; i < nout; ++i) {
-    FL_REQUIRE(outputs[i] != nullptr, "fl_gemv_bf16: null output");
+    FL_REQUIRE(outputs[i] != nullptr, w + ": null output");
     a.y[i] = outputs[i];
   }
-  if (epilogue == kEpiAdd) FL_REQUIRE(addend != nullptr && addend_stride >= n, "fl_gemv_bf16: bad addend");
-  if (epilogue == kEpiSwiGlu) FL_REQUIRE(n % 2 == 0, "fl_gemv_bf16: SwiGLU needs an even N");
+  if (epilogue == kEpiAdd) FL_REQUIRE(addend != nullptr && addend_stride >= n, w + ": bad addend");
+  if (epilogue == kEpiSwiGlu) FL_REQUIRE(n % 2 == 0, w + ": SwiGLU needs an even N");
   if (epilogue == kEpiRope)
     FL_REQUIRE(rope_cos && rope_sin && head_dim >= 8 && head_dim % 8 == 0 && n % head_dim == 0,
-               "fl_gemv_bf16: rope needs cos/sin tables and N a multiple of head_dim (multiple of 8)");
+               w + ": rope needs cos/sin tables and N a multiple of head_dim (multiple of 8)");
   a.x = x;
   a.x_f32 = x_is_f32 ? 1 : 0;
   a.x_stride = x_stride;
@@ -445,6 +572,26 @@ extern "C" int32_t fl_gemv_bf16(const void* x, int32_t x_is_f32, int64_t x_strid
   a.cos = rope_cos;
   a.sin = rope_sin;
   a.head_dim = head_dim;
+  return FL_OK;
+}
+
+int gemv_blocks(int epilogue, int n) {
+  return epilogue == kEpiSwiGlu ? n / 2 : (epilogue == kEpiRope ? 3 * (n / kRows) : n / kRows);
+}
+
+}  // namespace
+}  // namespace fl
+
+extern "C" int32_t fl_gemv_bf16(const void* x, int32_t x_is_f32, int64_t x_stride, int32_t m, int32_t k,
+                                const uint16_t* const* weights, int32_t n, int32_t epilogue, void* const* outputs,
+                                int64_t out_stride, const uint16_t* addend, int64_t addend_stride,
+                                const uint16_t* rope_cos, const uint16_t* rope_sin, int32_t head_dim, void* stream) {
+  using namespace fl;
+  clear_error();
+  GemvArgs a{};
+  const int32_t rc = make_gemv_args(a, x, x_is_f32, x_stride, m, k, weights, n, epilogue, outputs, out_stride, addend,
+                                    addend_stride, rope_cos, rope_sin, head_dim, "fl_gemv_bf16");
+  if (rc != FL_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (epilogue) {
     case kEpiPlain: launch_gemv<kEpiPlain>(a, n / kRows, st); break;
@@ -454,6 +601,40 @@ extern "C" int32_t fl_gemv_bf16(const void* x, int32_t x_is_f32, int64_t x_strid
     default: launch_gemv<kEpiRope>(a, 3 * (n / kRows), st); break;
   }
   FL_LAUNCH_CHECK("fl_gemv_bf16");
+  return FL_OK;
+}
+
+extern "C" int32_t fl_gemv_bf16_chain(int32_t m, int32_t k, float eps, const uint16_t* x, const uint16_t* r,
+                                      const uint16_t* w_a, const uint16_t* w_f, const uint16_t* w_b, uint16_t* h_out,
+                                      int64_t stride, const uint16_t* const* weights, int32_t n, int32_t epilogue,
+                                      void* const* outputs, int64_t out_stride, const uint16_t* addend,
+                                      int64_t addend_stride, const uint16_t* rope_cos, const uint16_t* rope_sin,
+                                      int32_t head_dim, void* stream) {
+  using namespace fl;
+  clear_error();
+  FL_REQUIRE(r != nullptr, "fl_gemv_bf16_chain: null residual/input");
+  FL_REQUIRE(k <= kChainMaxK && stride >= k && stride % 8 == 0,
+             "fl_gemv_bf16_chain: K must be at most 4096 and the chain row stride a multiple of 8 >= K");
+  FL_REQUIRE(x == nullptr || w_a != nullptr, "fl_gemv_bf16_chain: x needs its norm weight");
+  for (const void* p : {static_cast<const void*>(x), static_cast<const void*>(r), static_cast<const void*>(w_a),
+                        static_cast<const void*>(w_f), static_cast<const void*>(w_b), static_cast<const void*>(h_out)})
+    FL_REQUIRE(reinterpret_cast<uintptr_t>(p) % 16 == 0, "fl_gemv_bf16_chain: every chain tensor must be 16-byte aligned");
+  GemvArgs a{};
+  // the GEMV's x is the chain output: its checks run on the residual row layout
+  const int32_t rc = make_gemv_args(a, r, 0, stride, m, k, weights, n, epilogue, outputs, out_stride, addend,
+                                    addend_stride, rope_cos, rope_sin, head_dim, "fl_gemv_bf16_chain");
+  if (rc != FL_OK) return rc;
+  const NormArgs c{k, eps, x, r, w_a, w_f, w_b, h_out, nullptr, stride};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int blocks = gemv_blocks(epilogue, n);
+  switch (epilogue) {
+    case kEpiPlain: launch_gemv_chain<kEpiPlain>(a, c, blocks, st); break;
+    case kEpiF32: launch_gemv_chain<kEpiF32>(a, c, blocks, st); break;
+    case kEpiAdd: launch_gemv_chain<kEpiAdd>(a, c, blocks, st); break;
+    case kEpiSwiGlu: launch_gemv_chain<kEpiSwiGlu>(a, c, blocks, st); break;
+    default: launch_gemv_chain<kEpiRope>(a, c, blocks, st); break;
+  }
+  FL_LAUNCH_CHECK("fl_gemv_bf16_chain");
   return FL_OK;
 }
 

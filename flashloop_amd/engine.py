@@ -186,6 +186,9 @@ class FlashLoopEngine:
         self._runner = DecodeRunner(self, use_graphs)
         # decode-step model ops on the fused HIP kernels (False: torch modules)
         self.fused_decode = True
+        # with fused_decode: each residual/norm chain runs in the prologue of the GEMV that
+        # consumes it (False: separate fl_norm_chain launches; same results bit for bit)
+        self.fused_chain = True
         self._wcache = None
 
     @classmethod
@@ -389,7 +392,24 @@ class FlashLoopEngine:
         cos, sin = self.backbone.rotary_emb(h, pos_t)
         rope = (cos.reshape(bsz, hd), sin.reshape(bsz, hd))
         hid = h.reshape(bsz, -1)
-        _, z = kernels.norm_chain(hid, w_b=layers_w[0]["ln1"], eps=eps, want_h=False)
+        chained = self.fused_chain
+        # the chain whose output feeds the next GEMV: kwargs of norm_chain (h = hid + n_a(x),
+        # optional final norm, z = n_b(h)); it runs inside that GEMV when chained
+        pending = dict(w_b=layers_w[0]["ln1"])
+        first = True
+
+        def chain_gemv(weights, **gk):
+            nonlocal hid, first
+            if chained:
+                h_new, y = kernels.gemv_chain(hid, weights, eps=eps, want_h=not first, **pending, **gk)
+            else:
+                h_new, z = kernels.norm_chain(hid, eps=eps, want_h=not first, **pending)
+                y = kernels.gemv(h_new if pending.get("w_b") is None else z, weights, **gk)
+            if not first:
+                hid = h_new
+            first = False
+            return y
+
         cur_k = [[None] * 4 for _ in range(nl)]
         cur_v = [[None] * 4 for _ in range(nl)]
         sources: list[_LayerSource | None] = [None] * nl
@@ -397,8 +417,7 @@ class FlashLoopEngine:
             for li, layer in enumerate(self.layers):
                 w = layers_w[li]
                 a = layer.self_attn
-                q, k, v = kernels.gemv(z, [w["q"], w["k"], w["v"]], epilogue=kernels.EPI_ROPE, rope=rope,
-                                       head_dim=hd)
+                q, k, v = chain_gemv([w["q"], w["k"], w["v"]], epilogue=kernels.EPI_ROPE, rope=rope, head_dim=hd)
                 q, k, v = (t.view(bsz, heads, 1, hd) for t in (q, k, v))
                 cur_k[li][loop] = k
                 cur_v[li][loop] = v
@@ -425,16 +444,16 @@ class FlashLoopEngine:
                             scaling=a.scaling)
                     projected = kernels.gemv(delta.reshape(bsz, -1), [w["o"]], epilogue=kernels.EPI_ADD,
                                              addend=src.projected_output)
-                hid, z = kernels.norm_chain(hid, x=projected, w_a=w["ln2"], w_b=w["ln3"], eps=eps)
-                act = kernels.gemv(z, [w["gate"], w["up"]], epilogue=kernels.EPI_SWIGLU)
+                pending = dict(x=projected, w_a=w["ln2"], w_b=w["ln3"])
+                act = chain_gemv([w["gate"], w["up"]], epilogue=kernels.EPI_SWIGLU)
                 mo = kernels.gemv(act, [w["down"]])
                 last = li == nl - 1
                 nxt = None if (last and loop == 3) else layers_w[(li + 1) % nl]["ln1"]
-                hid, z = kernels.norm_chain(hid, x=mo, w_a=w["ln4"], w_f=extra["norm"] if last else None, w_b=nxt,
-                                            eps=eps)
+                pending = dict(x=mo, w_a=w["ln4"], w_f=extra["norm"] if last else None, w_b=nxt)
         for li in range(nl):
             cache.layers[li].append_rows(cur_k[li], cur_v[li])
-        return kernels.gemv(hid, [extra["lm_head"]], epilogue=kernels.EPI_F32)
+        # the last chain (final norm, no input norm) feeds lm_head
+        return chain_gemv([extra["lm_head"]], epilogue=kernels.EPI_F32)
 
     def _decode_core_modules(self, cache: CrossLoopKVCache, h: torch.Tensor, pos_t: torch.Tensor) -> torch.Tensor:
         """One decode step of ``B`` sequences on the device: every layer and loop, then the

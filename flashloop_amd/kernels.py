@@ -350,6 +350,46 @@ def norm_chain(r: torch.Tensor, *, x: torch.Tensor | None = None, w_a: torch.Ten
     return h, z
 
 
+def gemv_chain(r: torch.Tensor, weights, *, x: torch.Tensor | None = None, w_a: torch.Tensor | None = None,
+               w_f: torch.Tensor | None = None, w_b: torch.Tensor | None = None, eps: float, want_h: bool = True,
+               epilogue: int = EPI_PLAIN, addend: torch.Tensor | None = None,
+               rope: tuple[torch.Tensor, torch.Tensor] | None = None, head_dim: int = HEAD_DIM):
+    """``norm_chain`` followed by ``gemv`` of its output (z, or h without ``w_b``) in one
+    launch (``fl_gemv_bf16_chain``), bit-identical to the two calls.  Returns (h or None,
+    the GEMV output as ``gemv`` returns it)."""
+    r2 = _rows2d(r, "r")
+    m, d = r2.shape
+    x2 = None if x is None else _rows2d(x, "x")
+    for t, nm in ((r2, "r"), (x2, "x")):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError(f"{nm} must be bf16")
+    ws = [w if w.is_contiguous() else w.contiguous() for w in weights]
+    for w in ws:
+        _require(w, torch.bfloat16, "weight")
+    n = ws[0].shape[0]
+    dt = torch.float32 if epilogue == EPI_F32 else torch.bfloat16
+    nout = 3 if epilogue == EPI_ROPE else 1
+    outs = [torch.empty(m, n, dtype=dt, device=r2.device) for _ in range(nout)]
+    add = None
+    if epilogue == EPI_ADD:
+        add = addend.reshape(m, n)
+        _require(add, torch.bfloat16, "addend")
+    cos = sin = None
+    if epilogue == EPI_ROPE:
+        cos, sin = (t.reshape(m, head_dim).contiguous() for t in rope)
+        _require(cos, torch.bfloat16, "rope cos")
+        _require(sin, torch.bfloat16, "rope sin")
+    h = torch.empty(m, d, dtype=torch.bfloat16, device=r2.device) if want_h else None
+    rc = load().fl_gemv_bf16_chain(
+        m, d, float(eps), _p(x2), r2.data_ptr(), _p(w_a), _p(w_f), _p(w_b), _p(h), d,
+        C.cast(ptr_array([w.data_ptr() for w in ws]), _lib._PP), n, int(epilogue),
+        C.cast(ptr_array([o.data_ptr() for o in outs]), _lib._PP), n, _p(add), n, _p(cos), _p(sin), int(head_dim),
+        _stream(),
+    )
+    check(rc, "fl_gemv_bf16_chain")
+    return h, (tuple(outs) if epilogue == EPI_ROPE else outs[0])
+
+
 def append_tail(view, keys, values, tail_active, tail_tokens: torch.Tensor) -> None:
     """Device half of a decode append (``fl_append_tail``): rows ``keys[r]``/``values[r]``
     ([B, H, 1, 128] bf16, r = loop) to each sequence's tail at its device length."""

@@ -327,6 +327,21 @@ int32_t fl_append_tail(const fl_cache_view* view, const uint16_t* const* keys,
 int32_t fl_norm_chain(int32_t m, int32_t d, float eps, const uint16_t* x, const uint16_t* r,
                       const uint16_t* w_a, const uint16_t* w_f, const uint16_t* w_b,
                       uint16_t* h_out, uint16_t* z_out, int64_t stride, void* stream);
+/*
+ * fl_gemv_bf16_chain: fl_norm_chain followed by fl_gemv_bf16 in one launch (no reference
+ * counterpart: the engine's RMSNorm -> Linear module pairs, flashloop/engine.py:396-537,
+ * whose norm otherwise costs a launch of its own).  The GEMV's input rows are z of the
+ * chain (h when w_b is NULL), computed by every workgroup with the same arithmetic as
+ * fl_norm_chain (bit-identical results); h_out (optional) receives h.  The chain reads r
+ * and x (optional) with row stride `stride`; d = k <= 4096.  The GEMV arguments are
+ * those of fl_gemv_bf16 (x is the chain output, bf16).
+ */
+int32_t fl_gemv_bf16_chain(int32_t m, int32_t k, float eps, const uint16_t* x, const uint16_t* r,
+                           const uint16_t* w_a, const uint16_t* w_f, const uint16_t* w_b, uint16_t* h_out,
+                           int64_t stride, const uint16_t* const* weights, int32_t n, int32_t epilogue,
+                           void* const* outputs, int64_t out_stride, const uint16_t* addend,
+                           int64_t addend_stride, const uint16_t* rope_cos, const uint16_t* rope_sin,
+                           int32_t head_dim, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,5 +1,5 @@
-"""Fused decode-step model ops (fl_gemv_bf16, fl_norm_chain) against the torch modules
-they replace, and the fused engine step against the module step."""
+"""Fused decode-step model ops (fl_gemv_bf16, fl_norm_chain, fl_gemv_bf16_chain) against the
+torch modules they replace, and the fused engine step against the module step."""
 
 import pytest
 import torch
@@ -123,3 +123,57 @@ def test_fused_step_tracks_module_step():
         cos = F.cosine_similarity(a.double().flatten(), b.double().flatten(), dim=0).item()
         assert cos > 0.9999, f"step {i}: cos {cos}"
         assert (a - b).abs().max().item() < 2e-2 * max(1.0, b.abs().max().item()), f"step {i}"
+
+
+@pytest.mark.parametrize("k", [2048, 4096])
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_gemv_chain_is_norm_chain_then_gemv(m, k):
+    """fl_gemv_bf16_chain equals fl_norm_chain + fl_gemv_bf16 bit for bit (h and the
+    output), for every epilogue and every optional part of the chain."""
+    print(f"case: gemv chain m={m} k={k}", flush=True)
+    eps, hd = 1e-6, 128
+    wn = [(1.0 + 0.1 * _x(1, k, 40 + i, torch.float32)[0]).to(torch.bfloat16) for i in range(3)]
+    r, x = _x(m, k, 30), _x(m, k, 31) * 3.0
+    n = 512
+    mats = [_w(n, k, 50 + i) for i in range(3)]
+    pos = torch.arange(m, device=DEV) + 7
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2, device=DEV).float() / hd))
+    ang = torch.cat([pos[:, None] * inv[None], pos[:, None] * inv[None]], dim=-1)
+    rope = (ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16))
+    addend = _x(m, n, 32)
+    chains = [dict(x=x, w_a=wn[0], w_b=wn[2]), dict(x=x, w_a=wn[0], w_f=wn[1], w_b=wn[2]),
+              dict(w_b=wn[2]), dict(x=x, w_a=wn[0], w_f=wn[1])]
+    epis = [(kernels.EPI_PLAIN, mats[:1], {}), (kernels.EPI_F32, mats[:1], {}),
+            (kernels.EPI_ADD, mats[:1], dict(addend=addend)), (kernels.EPI_SWIGLU, mats[:2], {}),
+            (kernels.EPI_ROPE, mats, dict(rope=rope, head_dim=hd))]
+    for ci, ch in enumerate(chains):
+        h0, z0 = kernels.norm_chain(r, eps=eps, **ch)
+        inp = z0 if ch.get("w_b") is not None else h0
+        for epi, ws, extra in epis:
+            want = kernels.gemv(inp, ws, epilogue=epi, **extra)
+            h1, got = kernels.gemv_chain(r, ws, eps=eps, epilogue=epi, **ch, **extra)
+            assert torch.equal(h1, h0), f"chain {ci} epilogue {epi}: h differs"
+            for g_, w_ in zip(got if isinstance(got, tuple) else (got,), want if isinstance(want, tuple) else (want,)):
+                assert torch.equal(g_, w_), f"chain {ci} epilogue {epi}: output differs"
+    _, got = kernels.gemv_chain(r, mats[:1], eps=eps, want_h=False, w_b=wn[2])
+    _, z0 = kernels.norm_chain(r, eps=eps, w_b=wn[2], want_h=False)
+    assert torch.equal(got, kernels.gemv(z0, mats[:1]))
+
+
+def test_chained_step_equals_unchained_step():
+    """The engine's decode step with the chains inside the GEMVs equals the step with
+    separate chain launches bit for bit."""
+    tiny = OuroConfig(vocab_size=1024, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=2, num_key_value_heads=2)
+    model = OuroForCausalLM.random_init(tiny, seed=22, device=DEV)
+    g = torch.Generator().manual_seed(22)
+    ids = torch.randint(0, tiny.vocab_size, (1, 150), generator=g).to(DEV)
+    a_eng = FlashLoopEngine(model, use_graphs=False)
+    b_eng = FlashLoopEngine(model, use_graphs=False)
+    b_eng.fused_chain = False
+    a_eng.prefill(ids[:, :130], decode_capacity=64)
+    b_eng.prefill(ids[:, :130], decode_capacity=64)
+    for i in range(130, 150):
+        a = a_eng.decode(ids[:, i:i + 1]).logits
+        b = b_eng.decode(ids[:, i:i + 1]).logits
+        assert torch.equal(a, b), f"step {i}: max diff {(a - b).abs().max().item()}"
