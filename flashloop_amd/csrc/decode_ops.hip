@@ -57,6 +57,16 @@ __device__ __forceinline__ void unpack8(const uint4& u, float* f) {
   f[7] = bf16hi_to_f32(u.w);
 }
 
+// A raw buffer resource over `bytes` bytes at p (wave-uniform): loads past the end (or
+// from a resource of size 0) return zero.  Word 3 is the gfx9 raw-buffer format.
+using BufRes = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ BufRes buf_res(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(BufRes r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+}
+
 // x chunk q (8 values) of row m, as the bf16 values the Linear sees
 template <bool XF32>
 __device__ __forceinline__ void load_x8(const GemvArgs& a, int m, int q, float* f) {
@@ -245,6 +255,68 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
   gemv_finish<MT, EPI>(a, acc, red, mat, n0);
 }
 
+// The GEMV with every chunk a thread owns (S of them per row, K <= S * 2048) requested
+// at once as bounds-checked buffer loads: chunks past K and rows past M read as zero, so
+// no load sits under a branch (the compiler's wait after a branch join drains every
+// outstanding load).  Same accumulation order as gemv_kernel.
+template <int MT, int EPI, bool XF32, int S>
+__global__ __launch_bounds__(kGemvThreads) void gemv_flat_kernel(GemvArgs a) {
+  __shared__ float red[kGemvWaves][MT][kRows];
+  const uint16_t* rp[kRows];
+  int mat, n0;
+  block_rows<EPI>(a, blockIdx.x, rp, &mat, &n0);
+  constexpr int kStep = kGemvThreads;
+  constexpr uint32_t kXb = XF32 ? 4u : 2u;  // bytes per x element
+  const uint32_t q = threadIdx.x;
+  uint4 wv[S][kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const BufRes wr = buf_res(rp[r], static_cast<uint32_t>(a.K) * 2u);
+#pragma unroll
+    for (int s = 0; s < S; ++s) wv[s][r] = buf_load16(wr, 16u * (q + s * kStep));
+  }
+  uint4 xv[MT][S][XF32 ? 2 : 1];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const bool live = m < a.M;
+    const BufRes xr = buf_res(live ? static_cast<const char*>(a.x) + static_cast<int64_t>(m) * a.x_stride * kXb : nullptr,
+                              live ? static_cast<uint32_t>(a.K) * kXb : 0u);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const uint32_t off = 8u * kXb * (q + s * kStep);
+      xv[m][s][0] = buf_load16(xr, off);
+      if (XF32) xv[m][s][XF32 ? 1 : 0] = buf_load16(xr, off + 16u);
+    }
+  }
+  float acc[MT][kRows];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) acc[m][r] = 0.0f;
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      float x[8];
+      if (XF32) {
+        const uint4 u = xv[m][s][0], v = xv[m][s][XF32 ? 1 : 0];
+        const uint32_t w8[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = bf16_round(__uint_as_float(w8[e]));
+      } else {
+        unpack8(xv[m][s][0], x);
+      }
+#pragma unroll
+      for (int r = 0; r < kRows; ++r) {
+        float f[8];
+        unpack8(wv[s][r], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m][r] = fmaf(x[e], f[e], acc[m][r]);
+      }
+    }
+  gemv_finish<MT, EPI>(a, acc, red, mat, n0);
+}
+
 // ---------------------------------------------------------------------------------
 // Residual / RMSNorm chain of one row (one workgroup per row).  Thread t owns the
 // 8-value chunks t, t + 256, ... of the row; every global load (x, r and the three
@@ -310,16 +382,6 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 // written to h_out when write_h; then z = n_b(h) when n_b is given.  chain_load issues the
 // loads of this thread's chunks t, t + 256, ...; chain_finish leaves z (or h without n_b)
 // in v as bf16 values.  All kNormThreads threads must call chain_finish (block reductions).
-// A raw buffer resource over `bytes` bytes at p (wave-uniform): loads past the end (or
-// from a resource of size 0) return zero.  Word 3 is the gfx9 raw-buffer format.
-using BufRes = __amdgpu_buffer_rsrc_t;
-__device__ __forceinline__ BufRes buf_res(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
-}
-__device__ __forceinline__ uint4 buf_load16(BufRes r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
-}
-
 template <int NC>
 struct ChainIn {
   uint4 xr[NC], rr[NC], wa[NC], wf[NC], wb[NC];
@@ -491,12 +553,31 @@ __global__ __launch_bounds__(kAppendThreads) void append_tail_kernel(AppendArgs 
   if (threadIdx.x == 0) a.tail_tokens[b] = pos + 1;
 }
 
+template <int MT, int EPI, bool XF32>
+void launch_gemv_x(const GemvArgs& a, int blocks, hipStream_t st) {
+  const int steps = (a.K + kGemvThreads * 8 - 1) / (kGemvThreads * 8);
+  const dim3 g(blocks), t(kGemvThreads);
+  switch (steps) {
+    case 1: hipLaunchKernelGGL((gemv_flat_kernel<MT, EPI, XF32, 1>), g, t, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gemv_flat_kernel<MT, EPI, XF32, 2>), g, t, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((gemv_flat_kernel<MT, EPI, XF32, 3>), g, t, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((gemv_flat_kernel<MT, EPI, XF32, 4>), g, t, 0, st, a); break;
+    default: hipLaunchKernelGGL((gemv_kernel<MT, EPI, XF32>), g, t, 0, st, a); break;  // K > 8192
+  }
+}
+
 template <int MT, int EPI>
 void launch_gemv_m(const GemvArgs& a, int blocks, hipStream_t st) {
-  if (a.x_f32)
-    hipLaunchKernelGGL((gemv_kernel<MT, EPI, true>), dim3(blocks), dim3(kGemvThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL((gemv_kernel<MT, EPI, false>), dim3(blocks), dim3(kGemvThreads), 0, st, a);
+  if (MT > 2) {  // the flat form would hold MT x S x-chunks in registers
+    if (a.x_f32)
+      hipLaunchKernelGGL((gemv_kernel<MT, EPI, true>), dim3(blocks), dim3(kGemvThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((gemv_kernel<MT, EPI, false>), dim3(blocks), dim3(kGemvThreads), 0, st, a);
+  } else if (a.x_f32) {
+    launch_gemv_x<(MT > 2 ? 2 : MT), EPI, true>(a, blocks, st);
+  } else {
+    launch_gemv_x<(MT > 2 ? 2 : MT), EPI, false>(a, blocks, st);
+  }
 }
 
 template <int EPI>
