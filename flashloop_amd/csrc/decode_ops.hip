@@ -339,27 +339,37 @@ struct NormArgs {
   int64_t stride;      // row stride of every [M, D] tensor
 };
 
-__device__ __forceinline__ float norm_block_sum(float v, float* red) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float s = 0.0f;
+constexpr int kNormWaves = kNormThreads / kWave;
+
+// Block sums through two LDS buffers used in turn: reduction k writes buffer k & 1 and
+// every wave reads it before it reaches the barrier of reduction k + 1, so buffer k & 1 is
+// free again for reduction k + 2 -- one barrier per sum.
+struct BlockSum {
+  float (*red)[kNormWaves];
+  int phase;
+  __device__ __forceinline__ float operator()(float v) {
+    float* r = red[phase & 1];
+    ++phase;
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kNormThreads / kWave; ++i) s += red[i];
-  return s;
-}
+    for (int i = 0; i < kNormWaves; ++i) s += r[i];
+    return s;
+  }
+};
 
 // v <- RMSNorm(v) with weight chunks w (8 values per chunk), rounded to bf16
 template <int NC>
-__device__ __forceinline__ void rms_apply(float (*v)[8], const uint4* w, int nc, int D, float eps, float* red) {
+__device__ __forceinline__ void rms_apply(float (*v)[8], const uint4* w, int nc, int D, float eps, BlockSum& bs) {
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < NC; ++i)
     if (i < nc)
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(v[i][e], v[i][e], ss);
-  const float inv = rsqrtf(norm_block_sum(ss, red) / static_cast<float>(D) + eps);
+  const float inv = rsqrtf(bs(ss) / static_cast<float>(D) + eps);
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     float wf[8];
@@ -414,7 +424,7 @@ __device__ __forceinline__ void chain_load(const NormArgs& a, int64_t base, Chai
 
 template <int NC>
 __device__ __forceinline__ void chain_finish(const NormArgs& a, int64_t base, bool write_h, const ChainIn<NC>& in,
-                                             float (*h)[8], float* red) {
+                                             float (*h)[8], BlockSum& bs) {
   const int nc = (a.D / 8 - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;
 #pragma unroll
   for (int i = 0; i < NC; ++i) unpack8(in.rr[i], h[i]);
@@ -422,35 +432,36 @@ __device__ __forceinline__ void chain_finish(const NormArgs& a, int64_t base, bo
     float xv[NC][8];
 #pragma unroll
     for (int i = 0; i < NC; ++i) unpack8(in.xr[i], xv[i]);
-    rms_apply<NC>(xv, in.wa, nc, a.D, a.eps, red);
+    rms_apply<NC>(xv, in.wa, nc, a.D, a.eps, bs);
 #pragma unroll
     for (int i = 0; i < NC; ++i)
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[i][e] = bf16_round(h[i][e] + xv[i][e]);
   }
-  if (a.wf != nullptr) rms_apply<NC>(h, in.wf, nc, a.D, a.eps, red);
+  if (a.wf != nullptr) rms_apply<NC>(h, in.wf, nc, a.D, a.eps, bs);
   if (write_h && a.h_out != nullptr) {
 #pragma unroll
     for (int i = 0; i < NC; ++i)
       if (i < nc) reinterpret_cast<uint4*>(a.h_out + base)[threadIdx.x + i * kNormThreads] = pack8(h[i]);
   }
-  if (a.wb != nullptr) rms_apply<NC>(h, in.wb, nc, a.D, a.eps, red);
+  if (a.wb != nullptr) rms_apply<NC>(h, in.wb, nc, a.D, a.eps, bs);
 }
 
 template <int NC>
-__device__ __forceinline__ void chain_row(const NormArgs& a, int64_t base, bool write_h, float (*h)[8], float* red) {
+__device__ __forceinline__ void chain_row(const NormArgs& a, int64_t base, bool write_h, float (*h)[8], BlockSum& bs) {
   ChainIn<NC> in;
   chain_load<NC>(a, base, in);
-  chain_finish<NC>(a, base, write_h, in, h, red);
+  chain_finish<NC>(a, base, write_h, in, h, bs);
 }
 
 template <int NC>
 __global__ __launch_bounds__(kNormThreads) void norm_chain_kernel(NormArgs a) {
-  __shared__ float red[kNormThreads / kWave];
+  __shared__ float red[2][kNormWaves];
+  BlockSum bs{red, 0};
   const int64_t base = static_cast<int64_t>(blockIdx.x) * a.stride;
   const int nc = (a.D / 8 - static_cast<int>(threadIdx.x) + kNormThreads - 1) / kNormThreads;
   float h[NC][8];
-  chain_row<NC>(a, base, true, h, red);
+  chain_row<NC>(a, base, true, h, bs);
   if (a.wb != nullptr) {
 #pragma unroll
     for (int i = 0; i < NC; ++i)
@@ -470,7 +481,8 @@ static_assert(kGemvThreads == kNormThreads, "the chain prologue maps one GEMV th
 template <int MT, int EPI, int NC>
 __global__ __launch_bounds__(kGemvThreads) void gemv_chain_kernel(GemvArgs a, NormArgs c) {
   __shared__ float red[kGemvWaves][MT][kRows];
-  __shared__ float nred[kNormThreads / kWave];
+  __shared__ float nred[2][kNormWaves];
+  BlockSum bs{nred, 0};
   const uint16_t* rp[kRows];
   int mat, n0;
   block_rows<EPI>(a, blockIdx.x, rp, &mat, &n0);
@@ -499,9 +511,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_chain_kernel(GemvArgs a, No
     if (m < a.M) {
       float z[NC][8];
       if (m == 0)
-        chain_finish<NC>(c, 0, blockIdx.x == 0, in0, z, nred);
+        chain_finish<NC>(c, 0, blockIdx.x == 0, in0, z, bs);
       else
-        chain_row<NC>(c, static_cast<int64_t>(m) * c.stride, blockIdx.x == 0, z, nred);
+        chain_row<NC>(c, static_cast<int64_t>(m) * c.stride, blockIdx.x == 0, z, bs);
 #pragma unroll
       for (int s = 0; s < NC; ++s)
         if (q + s * kStep < nq)

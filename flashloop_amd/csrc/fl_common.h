@@ -48,12 +48,11 @@ __device__ __forceinline__ float bf16lo_to_f32(uint32_t w) { return __uint_as_fl
 __device__ __forceinline__ float bf16hi_to_f32(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x007FFFFFu)) {
-    return static_cast<uint16_t>((u >> 16) | 0x0040u);  // quiet NaN
-  }
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x0040u;  // quiet NaN, payload kept
+  const bool is_nan = (u & 0x7FFFFFFFu) > 0x7F800000u;
+  return static_cast<uint16_t>(is_nan ? qnan : rne);  // a select, not a branch per value
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
 
