@@ -420,45 +420,64 @@ __device__ void wave_tail(const DenseArgs& a, int bh, float (*comb)[kDim]) {
 #pragma unroll
   for (int c = 0; c < 32; ++c) st.acc[c] = 0.0f;
   const int n = tl + 1;
-  for (int base = 0; base < n; base += 16) {
+  // 16 tokens per step (lane = 4*row + quarter).  The next step's rows are requested
+  // while a step computes, from two named register sets (a copy of a set still in flight
+  // would wait for it); every load is unconditional: rows past the end read the current
+  // token's row and are masked.
+  struct Rows {
+    uint4 k[4], v[4];
+  };
+  auto fetch = [&](Rows& r, int base) __attribute__((always_inline)) {
     const int vt = base + row;
-    const bool valid = vt < n;
     const uint16_t* kr = (vt < tl) ? tk + static_cast<int64_t>(vt) * kDim : ck;
     const uint16_t* vr = (vt < tl) ? tv + static_cast<int64_t>(vt) * kDim : cv;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r.k[k] = *reinterpret_cast<const uint4*>(kr + 32 * quarter + 8 * k);
+      r.v[k] = *reinterpret_cast<const uint4*>(vr + 32 * quarter + 8 * k);
+    }
+  };
+  auto step = [&](const Rows& r, int base) __attribute__((always_inline)) {
+    const int vt = base + row;
+    const bool valid = vt < n;
     float d = 0.0f;
-    uint4 vwords[4];
-    if (valid) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint4 w = *reinterpret_cast<const uint4*>(kr + 32 * quarter + 8 * k);
-        d = fmaf(qr[8 * k + 0], bf16lo_to_f32(w.x), d);
-        d = fmaf(qr[8 * k + 1], bf16hi_to_f32(w.x), d);
-        d = fmaf(qr[8 * k + 2], bf16lo_to_f32(w.y), d);
-        d = fmaf(qr[8 * k + 3], bf16hi_to_f32(w.y), d);
-        d = fmaf(qr[8 * k + 4], bf16lo_to_f32(w.z), d);
-        d = fmaf(qr[8 * k + 5], bf16hi_to_f32(w.z), d);
-        d = fmaf(qr[8 * k + 6], bf16lo_to_f32(w.w), d);
-        d = fmaf(qr[8 * k + 7], bf16hi_to_f32(w.w), d);
-        vwords[k] = *reinterpret_cast<const uint4*>(vr + 32 * quarter + 8 * k);
-      }
-    } else {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) vwords[k] = make_uint4(0, 0, 0, 0);
+    for (int k = 0; k < 4; ++k) {
+      const uint4 w = r.k[k];
+      d = fmaf(qr[8 * k + 0], bf16lo_to_f32(w.x), d);
+      d = fmaf(qr[8 * k + 1], bf16hi_to_f32(w.x), d);
+      d = fmaf(qr[8 * k + 2], bf16lo_to_f32(w.y), d);
+      d = fmaf(qr[8 * k + 3], bf16hi_to_f32(w.y), d);
+      d = fmaf(qr[8 * k + 4], bf16lo_to_f32(w.z), d);
+      d = fmaf(qr[8 * k + 5], bf16hi_to_f32(w.z), d);
+      d = fmaf(qr[8 * k + 6], bf16lo_to_f32(w.w), d);
+      d = fmaf(qr[8 * k + 7], bf16hi_to_f32(w.w), d);
     }
     d = quad_sum(d);
     float lg = valid ? d : -INFINITY;
     if (LOGITS && quarter == 0 && valid) lrow[Tp + vt] = lg;
     float p;
     online_update(st, &lg, &p, 1);
+    p = valid ? p : 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t ws[4] = {vwords[k].x, vwords[k].y, vwords[k].z, vwords[k].w};
+      const uint32_t ws[4] = {r.v[k].x, r.v[k].y, r.v[k].z, r.v[k].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         st.acc[8 * k + 2 * e] = fmaf(p, bf16lo_to_f32(ws[e]), st.acc[8 * k + 2 * e]);
         st.acc[8 * k + 2 * e + 1] = fmaf(p, bf16hi_to_f32(ws[e]), st.acc[8 * k + 2 * e + 1]);
       }
     }
+  };
+  Rows ra, rb;
+  fetch(ra, 0);
+  for (int base = 0;; base += 32) {
+    fetch(rb, base + 16);
+    step(ra, base);
+    if (base + 16 >= n) break;
+    fetch(ra, base + 32);
+    step(rb, base + 16);
+    if (base + 32 >= n) break;
   }
   const float M = wave_max(st.m);  // finite: the current token is always present
   const float f = st.m == -INFINITY ? 0.0f : fast_exp2((st.m - M) * kLog2e);
