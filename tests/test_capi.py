@@ -46,6 +46,16 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == _lib.FL_E_INVALID
     rc = lib.fl_gather_rows(None, 0, 0, 0, None, 0, 0, 0, 0, None, 0, None, None)
     assert rc == _lib.FL_E_INVALID
+    # the fused chain + GEMV rejects its bad arguments before any launch
+    ws = _lib.ptr_array([0x1000])
+    outs = _lib.ptr_array([0x2000])
+    chain = lambda m, k, x, r, wa, stride: lib.fl_gemv_bf16_chain(
+        m, k, 1e-6, x, r, wa, None, None, None, stride, C.cast(ws, _lib._PP), 8, 0, C.cast(outs, _lib._PP), 8, None, 8,
+        None, None, 128, None)
+    assert chain(1, 2048, None, None, None, 2048) == _lib.FL_E_INVALID and b"null residual" in lib.fl_last_error()
+    assert chain(1, 8192, None, 0x3000, None, 8192) == _lib.FL_E_INVALID and b"4096" in lib.fl_last_error()
+    assert chain(1, 2048, 0x4000, 0x3000, None, 2048) == _lib.FL_E_INVALID and b"norm weight" in lib.fl_last_error()
+    assert chain(1, 2048, None, 0x3008, None, 2048) == _lib.FL_E_INVALID and b"aligned" in lib.fl_last_error()
 
 
 def test_struct_layout_matches_header(tmp_path):
