@@ -234,6 +234,16 @@ def test_decode_step_ragged_batch():
     _step_vs_oracle(w, layer)
 
 
+def test_decode_step_many_batches():
+    """More sequences than the readers cache lengths for in LDS (1024 dense, 512 gather):
+    the rows past the cache read their lengths from the device arrays."""
+    print("case: decode step ragged B1030 H1", flush=True)
+    lengths = ragged_lengths(1030, 65, 260, seed=5)
+    w = decode_workload(1030, 1, 0, seed=5, lengths=lengths)
+    layer = _build(w)
+    _step_vs_oracle(w, layer)
+
+
 def test_decode_step_full_fraction_equals_dense():
     """fraction 1 selects every key: loop-2 output + delta == dense loop-3/4 output."""
     print("case: full fraction", flush=True)
