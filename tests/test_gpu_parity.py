@@ -164,6 +164,37 @@ def test_topk_ragged_rows_and_budget_edges():
     assert np.allclose(mass.cpu().numpy(), sel.mass, rtol=2e-6)
 
 
+def test_topk_long_rows_and_large_budgets():
+    """Rows longer than the register-resident kernel holds (35840 keys) and budgets above
+    its selected-list capacity (8192) take the global-memory kernel; same bits."""
+    print("case: topk long rows", flush=True)
+    rng = np.random.default_rng(6)
+    n = 40000
+    lg = (rng.standard_normal((3, n)) * 2.0).astype(np.float32)
+    lg[1] = np.round(lg[1] * 4.0) / 4.0  # many exact ties
+    n_keys = [n, 36001, 20000]
+    for frac in (0.1, 0.3):
+        cap = max(OA.padded_capacity(OA.decode_budget(k, frac)) for k in n_keys)
+        t = torch.from_numpy(lg).to(DEV)
+        idx, valid, mass, wts, counts = kernels.decode_topk(t, torch.tensor(n_keys, dtype=torch.int32, device=DEV),
+                                                            frac, cap)
+        torch.cuda.synchronize()
+        sel = OA.decode_topk([lg[r, :k] for r, k in enumerate(n_keys)], frac, kpad=cap)
+        assert np.array_equal(idx.cpu().numpy(), sel.indices), f"indices differ at fraction {frac}"
+        assert np.array_equal(valid.cpu().numpy().astype(bool), sel.valid)
+        assert np.array_equal(counts.cpu().numpy(), sel.count)
+        assert np.allclose(mass.cpu().numpy(), sel.mass, rtol=2e-6)
+        assert np.allclose(wts.cpu().numpy(), sel.selected_weights, rtol=2e-5, atol=1e-8)
+    # a short row next to a long stride stays on its own key count
+    t = torch.from_numpy(lg).to(DEV)
+    short = torch.tensor([5, 64, 641], dtype=torch.int32, device=DEV)
+    cap = OA.padded_capacity(OA.decode_budget(641, 0.1))
+    idx, valid, mass, wts, counts = kernels.decode_topk(t, short, 0.1, cap)
+    torch.cuda.synchronize()
+    sel = OA.decode_topk([lg[r, :k] for r, k in enumerate([5, 64, 641])], 0.1, kpad=cap)
+    assert np.array_equal(idx.cpu().numpy(), sel.indices)
+
+
 def _step_vs_oracle(w, layer, m3=None, m4=None, frac=0.10):
     b, h = len(w.lengths), w.keys[0].shape[1]
     R = b * h
