@@ -1,4 +1,4 @@
-"""GPU parity at the shapes of BASELINE.json configs 0-2 (config 3 is the benchmark shape).
+"""GPU parity at the shapes of BASELINE.json configs 0-3.
 
 cfg0: B1 H16 T2048, one dense decode step over all four loops, fp32 outputs vs the oracle.
 cfg1: T8192 followed by 256 decode appends (a rollover every 64): the packed streams equal
@@ -8,6 +8,8 @@ cfg1: T8192 followed by 256 decode appends (a rollover every 64): the packed str
 cfg2: B32 H16, per-sequence contexts drawn from U[1024, 16384] (seeded): one decode step
       over the full ragged batch on the GPU; the rows of the shortest and the longest
       sequence (heads 0 and 15) are checked against the oracle.
+cfg3: B8 H16 T32768 (the benchmark shape): one decode step over every row; the first and
+      the last row are checked against the oracle (k = 3277 keys in loops 3-4).
 """
 
 import numpy as np
@@ -142,3 +144,49 @@ def test_cfg2_ragged_batch32():
                                    so, sel.mass, SCALING)
             assert_close(got[rows], want, what=f"cfg2 b={b} loop-{loop + 1} delta")
     assert Tmax <= 16384
+
+
+def test_cfg3_full_shape_rows():
+    """cfg3 at its full shape (B8 H16 T32768, the benchmark workload): one decode step over
+    every row on the GPU; two rows (first and last) are checked against the oracle."""
+    print("case: cfg3 B8 H16 T32768", flush=True)
+    B, H, T = 8, 16, 32768
+    w = decode_workload(B, H, T, seed=3)
+    layer = _layer([w.cache(r)[0] for r in range(4)], [w.cache(r)[1] for r in range(4)])
+    qs = [w.queries[r].to(DEV) for r in range(4)]
+    cur = [w.current(r) for r in range(4)]
+    step = decode_attention_step(layer, qs, [c[0].to(DEV) for c in cur], [c[1].to(DEV) for c in cur], SCALING, 0.10)
+    torch.cuda.synchronize()
+    R = B * H
+    out0 = np32(step.out0).reshape(R, 128)
+    out1 = np32(step.out1).reshape(R, 128)
+    d2 = np32(step.delta2).reshape(R, 128)
+    d3 = np32(step.delta3).reshape(R, 128)
+    g_lg = np32(step.logits1).reshape(R, -1)
+    cap = step.indices.shape[-1]
+    idx = step.indices.cpu().numpy().reshape(R, cap)
+    for a in (out0, out1, d2, d3):
+        assert np.isfinite(a).all()
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        ks = [w.keys[r][b:b + 1, h:h + 1, :T] for r in range(4)]
+        vs = [w.values[r][b:b + 1, h:h + 1, :T] for r in range(4)]
+        nk, nv, chain, tp = oracle_prefix(ks, vs)
+        Kb, Vb = materialized(nk, nv, chain, tp)
+        rows = [b * H + h]
+        q = [np32(w.queries[r]).reshape(R, 128)[rows] for r in range(4)]
+        kc = [np32(c[0]).reshape(R, 128)[rows] for c in cur]
+        vc = [np32(c[1]).reshape(R, 128)[rows] for c in cur]
+        Kr = [flat_rows(Kb[r]) for r in range(4)]
+        Vr = [flat_rows(Vb[r]) for r in range(4)]
+        o0, _ = OA.dense_decode(q[0], Kr[0], Vr[0], kc[0], vc[0], SCALING)
+        o1, _ = OA.dense_decode(q[1], Kr[1], Vr[1], kc[1], vc[1], SCALING)
+        assert_close(out0[rows], o0, what=f"cfg3 row {rows[0]} loop-1 output")
+        assert_close(out1[rows], o1, what=f"cfg3 row {rows[0]} loop-2 output")
+        sel = OA.decode_topk([g_lg[r, : T + 1] for r in rows], 0.10, kpad=cap)
+        assert np.array_equal(idx[rows], sel.indices), f"cfg3 row {rows[0]} selection"
+        assert sel.count[0] == 3277
+        so = OA.selected_value_aggregate(sel.indices, sel.valid, sel.selected_weights, Vr[1], vc[1], [T])
+        for loop, got in ((2, d2), (3, d3)):
+            want = OA.sparse_delta(q[loop], Kr[loop], Vr[loop], kc[loop], vc[loop], [T], sel.indices, sel.valid,
+                                   so, sel.mass, SCALING)
+            assert_close(got[rows], want, what=f"cfg3 row {rows[0]} loop-{loop + 1} delta")
