@@ -546,20 +546,35 @@ struct AppendArgs {
 __global__ __launch_bounds__(kAppendThreads) void append_tail_kernel(AppendArgs a) {
   const fl_cache_view& v = a.v;
   const int b = blockIdx.x;
+  constexpr int kChunks = kDim / 8;   // 16-byte chunks per row
+  const int per = v.heads * kChunks;  // chunks of one tensor for this sequence
+  // tensor t: loop t & 3, K for t < 4; t is a compile-time index in every use below (a
+  // runtime index into the argument arrays would load each pointer from memory first)
+  auto src_of = [&](int t, int i) __attribute__((always_inline)) {
+    const uint16_t* base = t < 4 ? a.k[t & 3] : a.val[t & 3];
+    const int h = i / kChunks, c = i - h * kChunks;
+    return reinterpret_cast<const uint4*>(base + (static_cast<int64_t>(b) * v.heads + h) * kDim) + c;
+  };
+  auto dst_of = [&](int t, int i, int pos) __attribute__((always_inline)) {
+    uint16_t* base = static_cast<uint16_t*>(t < 4 ? v.tail_key[t & 3] : v.tail_value[t & 3]);
+    const int h = i / kChunks, c = i - h * kChunks;
+    return reinterpret_cast<uint4*>(base + ((static_cast<int64_t>(b) * v.heads + h) * v.tail_capacity + pos) * kDim) +
+           c;
+  };
+  // chunk threadIdx.x of each of the 8 tensors is requested before the first store (the
+  // rows do not depend on the tail length, loaded alongside): one memory round trip
   const int pos = v.tail_tokens[b];
+  const int i0 = threadIdx.x;
+  uint4 held[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) held[t] = i0 < per ? *src_of(t, i0) : make_uint4(0, 0, 0, 0);
   if (pos < 0 || pos >= v.tail_capacity) return;  // the host rolls over before the tail is full
-  constexpr int kChunks = kDim / 8;              // 16-byte chunks per row
-  const int per = v.heads * kChunks;             // chunks of one tensor for this sequence
-  for (int i = threadIdx.x; i < 8 * per; i += kAppendThreads) {
-    const int t = i / per, rem = i - t * per;
-    const int h = rem / kChunks, c = rem - h * kChunks;
-    const int64_t row = static_cast<int64_t>(b) * v.heads + h;
-    const int loop = t & 3;
-    const uint16_t* src = (t < 4 ? a.k[loop] : a.val[loop]) + row * kDim;
-    uint16_t* dst = static_cast<uint16_t*>(t < 4 ? v.tail_key[loop] : v.tail_value[loop]) +
-                    (row * v.tail_capacity + pos) * kDim;
-    reinterpret_cast<uint4*>(dst)[c] = reinterpret_cast<const uint4*>(src)[c];
-  }
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+    if (i0 < per) *dst_of(t, i0, pos) = held[t];
+  for (int i = i0 + kAppendThreads; i < per; i += kAppendThreads)  // more than 16 heads
+#pragma unroll
+    for (int t = 0; t < 8; ++t) *dst_of(t, i, pos) = *src_of(t, i);
   if (threadIdx.x < 2) a.active[threadIdx.x][static_cast<int64_t>(b) * v.tail_capacity + pos] = 1;
   __syncthreads();
   if (threadIdx.x == 0) a.tail_tokens[b] = pos + 1;
