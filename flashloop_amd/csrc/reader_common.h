@@ -187,16 +187,33 @@ __device__ __forceinline__ float merge_channel_sum(const MergeParts& P, const fl
 __device__ __forceinline__ float merge_softmax_general(const MergeParts& P, MergeLdsBuf& S) {
   const int tid = threadIdx.x;
   const int n = min(P.count(), kMergeMaxParts);
+  // (m, l) of this thread's parts are loaded once, in one round, and kept in registers
+  constexpr int kPer = kMergeMaxParts / kMergeThreads;
+  float mi[kPer], li[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = tid + k * kMergeThreads;
+    mi[k] = -INFINITY;
+    li[k] = 0.0f;
+    if (i < n) {
+      const float* p = P.part(i);
+      mi[k] = p[0];
+      li[k] = p[1];
+    }
+  }
   float M = -INFINITY;
-  for (int i = tid; i < n; i += kMergeThreads) M = fmaxf(M, P.part(i)[0]);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) M = fmaxf(M, mi[k]);
   M = block_max_merge(M, S.red);
   float L = 0.0f;
-  for (int i = tid; i < n; i += kMergeThreads) {
-    const float* p = P.part(i);
-    const float m = p[0];
-    const float fi = (m == -INFINITY) ? 0.0f : fast_exp2((m - M) * kLog2e);
-    S.f[i] = fi;
-    L = fmaf(p[1], fi, L);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = tid + k * kMergeThreads;
+    if (i < n) {
+      const float fi = (mi[k] == -INFINITY) ? 0.0f : fast_exp2((mi[k] - M) * kLog2e);
+      S.f[i] = fi;
+      L = fmaf(li[k], fi, L);
+    }
   }
   L = block_sum_merge(L, S.red);  // also orders the f[] writes before the reads below
   const float acc = merge_channel_sum<true>(P, S.f, S.acc);
