@@ -67,6 +67,38 @@ def test_pack_bit_exact(masked):
         assert np.array_equal(got_v, chain.recon_values[r]), f"R_{r} values differ"
 
 
+@pytest.mark.parametrize("loops", [1, 2, 3])
+def test_pack_fewer_loops_match_the_four_loop_encode(loops):
+    """The C-ABI's 1..3-loop packs (one kernel per loop count) write exactly the first
+    streams of the 4-loop encode and leave the others untouched."""
+    print("case: pack B2 H3 T390 masked loops=%d" % loops, flush=True)
+    b, h, t = 2, 3, 390
+    w = decode_workload(b, h, t, seed=13)
+    m3, m4 = _masks(b, t, 7)
+    full = _build(w, m3, m4)
+    tp = full.quantized_tokens
+    part = CrossLoopKVLayer(full.geometry, DEV)
+    for s in range(2):
+        part.rank[s].copy_(full.rank[s])
+    ks = [w.cache(r)[0].to(DEV).reshape(b * h, t, 128).contiguous() for r in range(loops)]
+    vs = [w.cache(r)[1].to(DEV).reshape(b * h, t, 128).contiguous() for r in range(loops)]
+    mk = [torch.from_numpy(m).to(DEV).to(torch.uint8).contiguous() for m in (m3, m4)]
+    kernels.pack_kv_groups(part.view(), loops, ks, vs, src_bh_stride=t, src_row_offset=0,
+                           dst_group0=torch.zeros(b, dtype=torch.int32, device=DEV), n_groups=tp // 64,
+                           masks=mk, mask_stride=t)
+    torch.cuda.synchronize()
+    for s in range(4):
+        same = s < loops
+        for name in ("codes", "key_meta", "value_meta", "key_meta_half", "value_meta_half"):
+            got, ref = getattr(part, name)[s], getattr(full, name)[s]
+            if same:
+                assert torch.equal(got, ref), f"stream {s} {name} differs"
+            else:
+                assert not torch.any(got != 0), f"stream {s} {name} written by a {loops}-loop pack"
+        rec_got, rec_ref = part.value_meta_token[..., s, :], full.value_meta_token[..., s, :]
+        assert torch.equal(rec_got, rec_ref) if same else not torch.any(rec_got != 0)
+
+
 def test_pack_closed_forms():
     """Constant and ramp groups through the GPU codec (known answers)."""
     print("case: pack closed forms", flush=True)
