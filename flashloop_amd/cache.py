@@ -262,6 +262,16 @@ class CrossLoopKVLayer:
             logits = logits.view(self.batch, self.heads, 1, -1)
         return out, logits
 
+    def dense_source_attention_pair(self, *, queries, current_keys, current_values, scaling: float):
+        """Loops 1 and 2 of ``dense_source_attention`` (loop 2 with logits) in one reader
+        launch (``fl_decode_attn_dense_pair``).  Returns ``(out loop 1, out loop 2, logits)``
+        shaped as ``dense_source_attention`` returns them."""
+        out0, out1, logits = kernels.fused_dense_pair(
+            self.view(), queries, current_keys, current_values, scaling,
+            logits_capacity=self.logits_capacity(), device=self.device, workspace=self.workspace)
+        shape = (self.batch, self.heads, 1, HEAD_DIM)
+        return out0.view(shape), out1.view(shape), logits.view(self.batch, self.heads, 1, -1)
+
     def key_counts(self) -> torch.Tensor:
         """Keys per sequence including the current token: packed + tail + 1 (device)."""
         return self.packed_tokens + self.tail_tokens + 1
@@ -592,7 +602,8 @@ class AttentionStep:
 
 
 def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scaling: float,
-                          fraction: float = 0.10, fused_source: bool = True) -> AttentionStep:
+                          fraction: float = 0.10, fused_source: bool = True,
+                          paired_dense: bool = True) -> AttentionStep:
     """One layer's decode attention over four loops (flashloop/engine.py:422-531, before
     ``o_proj``): dense loops 1-2 (loop 2 with logits), loop-2 key selection and selected
     aggregate, then the cached-mass deltas of loops 3-4.  ``queries/keys/values``: four
@@ -600,11 +611,16 @@ def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scalin
 
     With ``fused_source`` the loop-2 selected aggregate is formed by the loop-3 reader
     from the rows it reads anyway (it is first consumed there, engine.py:511-528);
-    otherwise it is a separate selected-PV pass at loop 2, as in the reference."""
-    out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=keys[0], current_value=values[0],
-                                           scaling=scaling, return_logits=False)
-    out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=keys[1], current_value=values[1],
-                                                scaling=scaling, return_logits=True)
+    otherwise it is a separate selected-PV pass at loop 2, as in the reference.  With
+    ``paired_dense`` the two dense loops share one reader launch."""
+    if paired_dense:
+        out0, out1, logits = layer.dense_source_attention_pair(
+            queries=queries[:2], current_keys=keys[:2], current_values=values[:2], scaling=scaling)
+    else:
+        out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=keys[0], current_value=values[0],
+                                               scaling=scaling, return_logits=False)
+        out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=keys[1],
+                                                    current_value=values[1], scaling=scaling, return_logits=True)
     idx, valid, mass, w, counts = layer.select_decode_keys(logits, fraction)
     if fused_source:
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(

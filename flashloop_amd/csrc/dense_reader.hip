@@ -558,29 +558,27 @@ __device__ __forceinline__ void stage_partial(const WaveState& st, float* part) 
   }
 }
 
-// At most two waves per SIMD: a tighter register budget makes the compiler spill the
-// ping-pong load sets to scratch (measured: the loop-1 reader 126 -> 154 us).
+// The LDS of one reader workgroup.
 template <int NS, bool LOGITS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void dense_reader_kernel(DenseArgs a) {
-  __shared__ WaveLds<NS> sh[kWaves];
-  __shared__ float lgsh[LOGITS ? kWaves : 1][LOGITS ? kStageGroups * kGroup : 1];
-  __shared__ float psh[kWaves][kStageSegs][kPartial];
-  __shared__ SegMeta segsh[kWaves][kStageSegs];
+struct ReaderLds {
+  WaveLds<NS> sh[kWaves];
+  float lgsh[LOGITS ? kWaves : 1][LOGITS ? kStageGroups * kGroup : 1];
+  float psh[kWaves][kStageSegs][kPartial];
+  SegMeta segsh[kWaves][kStageSegs];
+};
+
+// Wave w's units [u0, u1) of one loop's work sequence.
+template <int NS, bool LOGITS>
+__device__ __forceinline__ void dense_range(const DenseArgs& a, ReaderLds<NS, LOGITS>& L, const RowLens& rl, int w,
+                                            int64_t u0, int64_t u1) {
+  if (u0 >= u1) return;
   const fl_cache_view& v = a.v;
   const int wave = threadIdx.x >> 6;
-  const int w = blockIdx.x * kWaves + wave;
-  const int W = a.waves;
   const int BH = v.batch * v.heads;
-
-  __shared__ int lens[kLenCache];
-  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kThreads) lens[i] = row_groups(v, i);
-  __syncthreads();
-  const RowLens rl{lens, min(v.batch, kLenCache)};
-  const int64_t U = total_units(v, rl);
-  const int64_t chunk = chunk_of(U, W);
-  const int64_t u0 = static_cast<int64_t>(w) * chunk;
-  const int64_t u1 = min(u0 + chunk, U);
-  if (u0 >= u1) return;
+  auto& sh = L.sh;
+  auto& lgsh = L.lgsh;
+  auto& psh = L.psh;
+  auto& segsh = L.segsh;
 
   // Tails whose first unit lies in [u0, u1), then the count of prefix groups in range.
   Cursor c = locate(v, rl, u0);
@@ -667,15 +665,67 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
   stage_flush<LOGITS>(a, seg, nseg, lgbuf, pbuf, w, false);
 }
 
+// At most two waves per SIMD: a tighter register budget makes the compiler spill the
+// ping-pong load sets to scratch (measured: the loop-1 reader 126 -> 154 us).
+template <int NS, bool LOGITS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void dense_reader_kernel(DenseArgs a) {
+  __shared__ ReaderLds<NS, LOGITS> L;
+  __shared__ int lens[kLenCache];
+  const fl_cache_view& v = a.v;
+  const int w = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kThreads) lens[i] = row_groups(v, i);
+  __syncthreads();
+  const RowLens rl{lens, min(v.batch, kLenCache)};
+  const int64_t U = total_units(v, rl);
+  const int64_t chunk = chunk_of(U, a.waves);
+  const int64_t u0 = static_cast<int64_t>(w) * chunk;
+  dense_range<NS, LOGITS>(a, L, rl, w, u0, min(u0 + chunk, U));
+}
+
+// Loops 1 and 2 of a decode step in one persistent launch (loop 2 with logits).  Their
+// work sequences are equal (streams 0 and 1 both cover the packed prefix); laid end to
+// end, they are split evenly over the waves, so the spread of the waves' end times is
+// paid once instead of once per loop.  Units [0, U) are loop 1's, [U, 2U) loop 2's; a
+// wave's partials go to its loop's workspace at the slots of its global wave index.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void dense_pair_kernel(DenseArgs a0,
+                                                                                                    DenseArgs a1) {
+  __shared__ ReaderLds<2, true> L;
+  __shared__ int lens[kLenCache];
+  static_assert(sizeof(ReaderLds<1, false>) <= sizeof(ReaderLds<2, true>), "loop-1 LDS must fit in loop-2 LDS");
+  const fl_cache_view& v = a0.v;
+  const int w = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kThreads) lens[i] = row_groups(v, i);
+  __syncthreads();
+  const RowLens rl{lens, min(v.batch, kLenCache)};
+  const int64_t U = total_units(v, rl);
+  const int64_t chunk = chunk_of(2 * U, a0.waves);
+  const int64_t u0 = static_cast<int64_t>(w) * chunk, u1 = min(u0 + chunk, 2 * U);
+  dense_range<1, false>(a0, *reinterpret_cast<ReaderLds<1, false>*>(&L), rl, w, u0, min(u1, U));
+  // The two loops view the same LDS through different types, which type-based alias
+  // analysis takes as disjoint: without a compiler barrier, loop 2's first LDS writes
+  // could be scheduled above loop 1's last staging reads (that corrupted the last loop-1
+  // row of the wave whose range crosses into loop 2).  The memory clobber orders every
+  // access; the wait completes loop 1's LDS reads.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  dense_range<2, true>(a1, L, rl, w, max(u0, U) - U, max(u1, U) - U);
+}
+
 // Combine row bh's partials: prefix slots [f+bh, l+bh] (see partial_slot) + its tail slot.
-__global__ __launch_bounds__(kMergeThreads) void dense_merge_kernel(const float* ws, int W, fl_cache_view v, float* out) {
+// `pieces` loops were read by one launch (dense_pair_kernel: 2): block p*BH + bh merges
+// row bh of piece p, whose units follow those of the earlier pieces.
+__global__ __launch_bounds__(kMergeThreads) void dense_merge_kernel(const float* ws0, const float* ws1, int W,
+                                                                    fl_cache_view v, float* out0, float* out1,
+                                                                    int pieces) {
   __shared__ int lens[kLenCache];
   __shared__ MergeLdsBuf S;
   for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kMergeThreads) lens[i] = row_groups(v, i);
   __syncthreads();
   const RowLens rl{lens, min(v.batch, kLenCache)};
-  const int bh = blockIdx.x;
   const int BH = v.batch * v.heads;
+  const int piece = blockIdx.x / BH;
+  const int bh = blockIdx.x - piece * BH;
+  const float* ws = piece == 0 ? ws0 : ws1;
+  float* out = piece == 0 ? out0 : out1;
   const int b = bh / v.heads, h = bh - (bh / v.heads) * v.heads;
   int64_t vs = 0, U = 0;
   for (int bb = 0; bb < v.batch; ++bb) {
@@ -684,10 +734,10 @@ __global__ __launch_bounds__(kMergeThreads) void dense_merge_kernel(const float*
     U += span;
   }
   const int gb = rl(v, b);
-  vs += static_cast<int64_t>(h) * (kTailUnits + gb);
+  vs += static_cast<int64_t>(h) * (kTailUnits + gb) + piece * U;
   int64_t f = 0, l = -1;
   if (gb > 0) {
-    const int64_t chunk = chunk_of(U, W);
+    const int64_t chunk = chunk_of(pieces * U, W);
     f = (vs + kTailUnits) / chunk;
     l = (vs + kTailUnits + gb - 1) / chunk;
   }
@@ -729,6 +779,20 @@ int occupancy() {
   return cached[dev];
 }
 
+int occupancy_pair() {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
+  std::lock_guard<std::mutex> g(mu);
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, dense_pair_kernel, kThreads, 0) != hipSuccess || n <= 0) n = 1;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int occupancy_of(int loop, bool logits) {
   switch (loop * 2 + (logits ? 1 : 0)) {
     case 0: return occupancy<1, false>();
@@ -742,7 +806,8 @@ int occupancy_of(int loop, bool logits) {
   }
 }
 
-constexpr int kMaxResident = 2;  // workgroups per CU any reader instantiation can hold
+constexpr int kMaxResident = 2;
+constexpr int kProfilePair = 4;  // fl_profile_dense_reader code of the pair launch  // workgroups per CU any reader instantiation can hold
 
 // ---- measurement hook (fl_profile_dense_reader): HIP events around the reader kernel
 struct ReaderProfile {
@@ -841,12 +906,11 @@ extern "C" size_t fl_decode_attn_dense_workspace(const fl_cache_view* view) {
   return static_cast<size_t>(waves + 2 * rows) * kPartial * sizeof(float);
 }
 
-extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop, const uint16_t* q,
-                                        const uint16_t* k_cur, const uint16_t* v_cur, float scaling, float* out,
-                                        float* logits, int64_t logits_stride, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
-  using namespace fl;
-  clear_error();
+namespace fl {
+namespace {
+// Argument checks of one dense read (loop `loop`, logits optional).
+int32_t dense_checks(const fl_cache_view* view, int32_t loop, const uint16_t* q, const uint16_t* k_cur,
+                     const uint16_t* v_cur, float* out, float* logits, int64_t logits_stride, void* workspace) {
   FL_REQUIRE(view != nullptr, "fl_decode_attn_dense: view is null");
   const fl_cache_view& v = *view;
   FL_REQUIRE(loop >= 0 && loop <= 3, "fl_decode_attn_dense: loop must be in 0..3");
@@ -865,8 +929,22 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   }
   FL_REQUIRE(logits == nullptr || logits_stride >= static_cast<int64_t>(v.max_packed_tokens) + v.max_tail_tokens + 1,
              "fl_decode_attn_dense: logits_stride smaller than the key count");
-  FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense: workspace too small");
   FL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "fl_decode_attn_dense: workspace must be 16-byte aligned");
+  return FL_OK;
+}
+}  // namespace
+}  // namespace fl
+
+extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop, const uint16_t* q,
+                                        const uint16_t* k_cur, const uint16_t* v_cur, float scaling, float* out,
+                                        float* logits, int64_t logits_stride, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  using namespace fl;
+  clear_error();
+  if (const int32_t rc = dense_checks(view, loop, q, k_cur, v_cur, out, logits, logits_stride, workspace); rc != FL_OK)
+    return rc;
+  const fl_cache_view& v = *view;
+  FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense: workspace too small");
   DenseArgs a{};
   a.v = v;
   a.q = q;
@@ -899,7 +977,59 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   profile_after(st);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(reader)");
   hipLaunchKernelGGL(dense_merge_kernel, dim3(v.batch * v.heads), dim3(kMergeThreads), 0, st,
-                     static_cast<const float*>(a.ws), a.waves, v, out);
+                     static_cast<const float*>(a.ws), static_cast<const float*>(a.ws), a.waves, v, out, out, 1);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(merge)");
+  return FL_OK;
+}
+
+namespace {
+// Byte offset of the second loop's partials in a pair workspace (256-byte aligned).
+size_t pair_half(const fl_cache_view* view) { return (fl_decode_attn_dense_workspace(view) + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" size_t fl_decode_attn_dense_pair_workspace(const fl_cache_view* view) {
+  return view ? 2 * pair_half(view) : 0;
+}
+
+extern "C" int32_t fl_decode_attn_dense_pair(const fl_cache_view* view, const uint16_t* q0, const uint16_t* k_cur0,
+                                             const uint16_t* v_cur0, float* out0, const uint16_t* q1,
+                                             const uint16_t* k_cur1, const uint16_t* v_cur1, float* out1,
+                                             float scaling, float* logits1, int64_t logits_stride, void* workspace,
+                                             size_t workspace_bytes, void* stream) {
+  using namespace fl;
+  clear_error();
+  if (const int32_t rc = dense_checks(view, 0, q0, k_cur0, v_cur0, out0, nullptr, 0, workspace); rc != FL_OK) return rc;
+  if (const int32_t rc = dense_checks(view, 1, q1, k_cur1, v_cur1, out1, logits1, logits_stride, workspace); rc != FL_OK)
+    return rc;
+  FL_REQUIRE(logits1 != nullptr, "fl_decode_attn_dense_pair: loop-2 logits are required");
+  FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_pair_workspace(view), "fl_decode_attn_dense_pair: workspace too small");
+  const fl_cache_view& v = *view;
+  DenseArgs a[2]{};
+  const uint16_t* qs[2] = {q0, q1};
+  const uint16_t* ks[2] = {k_cur0, k_cur1};
+  const uint16_t* vs[2] = {v_cur0, v_cur1};
+  const int blocks = persist_blocks(v, occupancy_pair());
+  for (int r = 0; r < 2; ++r) {
+    a[r].v = v;
+    a[r].q = qs[r];
+    a[r].kc = ks[r];
+    a[r].vc = vs[r];
+    a[r].scaling = scaling;
+    a[r].logits = r == 1 ? logits1 : nullptr;
+    a[r].logits_stride = r == 1 ? logits_stride : 0;
+    a[r].ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + r * pair_half(view));
+    a[r].tail_k = v.tail_key[r];
+    a[r].tail_v = v.tail_value[r];
+    a[r].waves = blocks * kWaves;
+  }
+  FL_REQUIRE(a[0].waves + 2 <= kMergeMaxParts, "fl_decode_attn_dense_pair: too many persistent waves for one merge");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  profile_before(st, kProfilePair);
+  hipLaunchKernelGGL(dense_pair_kernel, dim3(blocks), dim3(kThreads), 0, st, a[0], a[1]);
+  profile_after(st);
+  FL_LAUNCH_CHECK("fl_decode_attn_dense_pair(reader)");
+  hipLaunchKernelGGL(dense_merge_kernel, dim3(2 * v.batch * v.heads), dim3(kMergeThreads), 0, st,
+                     static_cast<const float*>(a[0].ws), static_cast<const float*>(a[1].ws), a[0].waves, v, out0, out1, 2);
+  FL_LAUNCH_CHECK("fl_decode_attn_dense_pair(merge)");
   return FL_OK;
 }

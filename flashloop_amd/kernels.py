@@ -77,6 +77,29 @@ class Workspace:
 _WS = Workspace()
 
 
+def fused_dense_pair(view, queries, keys, values, scaling, *, logits_capacity, device,
+                     workspace: Workspace | None = None):
+    """Loops 1 and 2 of a decode step in one reader launch (``fl_decode_attn_dense_pair``).
+    Returns (out loop 1 f32 [B*H,128], out loop 2, loop-2 logits f32 [B*H, logits_capacity])."""
+    lib = load()
+    rows = view.batch * view.heads
+    qs = [_vec(x, rows, "query") for x in queries]
+    ks = [_vec(x, rows, "current_key") for x in keys]
+    vs = [_vec(x, rows, "current_value") for x in values]
+    out0 = torch.empty(rows, HEAD_DIM, dtype=torch.float32, device=device)
+    out1 = torch.empty(rows, HEAD_DIM, dtype=torch.float32, device=device)
+    logits = torch.empty(rows, logits_capacity, dtype=torch.float32, device=device)
+    ws_bytes = lib.fl_decode_attn_dense_pair_workspace(C.byref(view))
+    ws = (workspace or _WS).get(ws_bytes, device)
+    rc = lib.fl_decode_attn_dense_pair(
+        C.byref(view), qs[0].data_ptr(), ks[0].data_ptr(), vs[0].data_ptr(), out0.data_ptr(),
+        qs[1].data_ptr(), ks[1].data_ptr(), vs[1].data_ptr(), out1.data_ptr(), float(scaling),
+        logits.data_ptr(), logits.shape[1], ws.data_ptr(), ws.numel(), _stream(),
+    )
+    check(rc, "fl_decode_attn_dense_pair")
+    return out0, out1, logits
+
+
 def fused_dense_source_attention(view, loop, query, current_key, current_value, scaling, *, return_logits,
                                  logits_capacity, device, workspace: Workspace | None = None, out=None, logits=None):
     """``dense_source_attention_cuda`` replacement.  Returns (out f32 [B*H,128], logits or None)."""

@@ -152,6 +152,22 @@ int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
                              float scaling, float* out, float* logits, int64_t logits_stride,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* Loops 1 and 2 of a decode step (streams 0 and 1; loop 2 with logits) in one reader
+ * launch plus one merge launch.  Same results as fl_decode_attn_dense(loop 0) followed by
+ * fl_decode_attn_dense(loop 1, logits): logits bit-identical, outputs within float
+ * rounding of the partial sums (the split points differ).  No counterpart in the
+ * reference, whose step calls dense_source_attention once per loop
+ * (flashloop/engine.py:420-436): fusing the two launches pays the end-of-launch
+ * imbalance of the persistent grid once.  logits1 is required.
+ * workspace: fl_decode_attn_dense_pair_workspace() bytes (16-byte aligned, any content).
+ */
+size_t fl_decode_attn_dense_pair_workspace(const fl_cache_view* view);
+int32_t fl_decode_attn_dense_pair(const fl_cache_view* view,
+                                  const uint16_t* q0, const uint16_t* k_cur0, const uint16_t* v_cur0, float* out0,
+                                  const uint16_t* q1, const uint16_t* k_cur1, const uint16_t* v_cur1, float* out1,
+                                  float scaling, float* logits1, int64_t logits_stride,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * Measurement hook (no counterpart in the reference; for benchmarks): record a pair of
  * HIP events on the launch stream immediately around the reader kernel (not the merge)
