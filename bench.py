@@ -52,8 +52,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline: repeat the sample's step until this much CPU time has run")
     ap.add_argument("--eager", action="store_true", help="cfg4: eager decode launches instead of HIP-graph replay")
-    ap.add_argument("--separate-dense", action="store_true",
-                    help="cfg3: dense loops 1 and 2 as two reader launches instead of one pair launch")
+    ap.add_argument("--paired-dense", action="store_true",
+                    help="cfg3: dense loops 1 and 2 in one pair launch (needs both loops' queries at "
+                         "once, which the looped model's loop-by-loop order never provides)")
     ap.add_argument("--no-chain", action="store_true",
                     help="cfg4: residual/norm chains as launches of their own, not inside the next GEMV")
     ap.add_argument("--fraction", type=float, default=0.10)
@@ -202,17 +203,17 @@ def main():
 
     def step():
         return decode_attention_step(layer, queries, kcur, vcur, SCALING, args.fraction,
-                                     paired_dense=not args.separate_dense)
+                                     paired_dense=args.paired_dense)
 
-    # the dense reader kernel (the loops 1+2 pair launch, or the loop-2 launch with
-    # --separate-dense) is timed by the library: HIP events recorded on the launch stream
+    # the dense reader kernel (the loop-2 launch, or the loops 1+2 pair launch with
+    # --paired-dense) is timed by the library: HIP events recorded on the launch stream
     # around that kernel in each timed step (fl_profile_dense_reader; code 4 = the pair)
     from flashloop_amd import _lib
 
     lib = _lib.load()
 
     def timed_step(i):
-        if args.separate_dense:
+        if (not args.paired_dense):
             out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=kcur[0], current_value=vcur[0],
                                                    scaling=SCALING, return_logits=False)
             out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=kcur[1],
@@ -233,7 +234,7 @@ def main():
         step()
     ref = step()
     torch.cuda.synchronize()
-    _lib.check(lib.fl_profile_dense_reader(1 if args.separate_dense else 4, args.steps), "fl_profile_dense_reader")
+    _lib.check(lib.fl_profile_dense_reader(1 if (not args.paired_dense) else 4, args.steps), "fl_profile_dense_reader")
     t0 = time.perf_counter()
     for i in range(args.steps):
         timed_step(i)
@@ -244,7 +245,7 @@ def main():
 
     tot_ms, n_rec = ctypes.c_float(0.0), ctypes.c_int32(0)
     _lib.check(lib.fl_profile_dense_reader_read(ctypes.byref(tot_ms), ctypes.byref(n_rec)), "fl_profile_dense_reader_read")
-    _lib.check(lib.fl_profile_dense_reader(1 if args.separate_dense else 4, 0), "fl_profile_dense_reader")
+    _lib.check(lib.fl_profile_dense_reader(1 if (not args.paired_dense) else 4, 0), "fl_profile_dense_reader")
     if n_rec.value != args.steps:
         raise RuntimeError(f"expected {args.steps} profiled loop-2 reader launches, got {n_rec.value}")
     reader_ms = tot_ms.value / n_rec.value
@@ -265,7 +266,7 @@ def main():
     }
     step_bytes = sum(parts.values())
     gbps = step_bytes / (ms_step * 1e-3) / 1e9
-    reader_bytes = parts["dense_loop2"] + (0 if args.separate_dense else parts["dense_loop1"])
+    reader_bytes = parts["dense_loop2"] + (0 if (not args.paired_dense) else parts["dense_loop1"])
     reader_gbps = reader_bytes / (reader_ms * 1e-3) / 1e9
     finite = all(bool(torch.isfinite(t).all()) for t in (ref.out0, ref.out1, ref.delta2, ref.delta3))
 
@@ -310,13 +311,13 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": ("dense_reader_kernel<2,true> (loop-2 dense reader)" if args.separate_dense
+            "kernel": ("dense_reader_kernel<2,true> (loop-2 dense reader)" if (not args.paired_dense)
                        else "dense_pair_kernel (loops 1+2 dense reader, one launch)"),
             "achieved": round(reader_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(reader_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": MEASURED_TRAFFIC.get(args.config if args.separate_dense else args.config + "-pair"),
+            "traffic": MEASURED_TRAFFIC.get(args.config if (not args.paired_dense) else args.config + "-pair"),
             "algorithmic_bytes": reader_bytes,
             "avg_us": round(reader_ms * 1e3, 2),
         },

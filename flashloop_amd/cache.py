@@ -603,7 +603,7 @@ class AttentionStep:
 
 def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scaling: float,
                           fraction: float = 0.10, fused_source: bool = True,
-                          paired_dense: bool = True) -> AttentionStep:
+                          paired_dense: bool = False) -> AttentionStep:
     """One layer's decode attention over four loops (flashloop/engine.py:422-531, before
     ``o_proj``): dense loops 1-2 (loop 2 with logits), loop-2 key selection and selected
     aggregate, then the cached-mass deltas of loops 3-4.  ``queries/keys/values``: four
@@ -612,7 +612,9 @@ def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scalin
     With ``fused_source`` the loop-2 selected aggregate is formed by the loop-3 reader
     from the rows it reads anyway (it is first consumed there, engine.py:511-528);
     otherwise it is a separate selected-PV pass at loop 2, as in the reference.  With
-    ``paired_dense`` the two dense loops share one reader launch."""
+    ``paired_dense`` the two dense loops share one reader launch; that needs both loops'
+    queries at once, which a looped model's decode (every layer of loop 1 before loop 2,
+    flashloop/engine.py:393-394) never has."""
     if paired_dense:
         out0, out1, logits = layer.dense_source_attention_pair(
             queries=queries[:2], current_keys=keys[:2], current_values=values[:2], scaling=scaling)

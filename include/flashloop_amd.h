@@ -156,9 +156,10 @@ int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
  * launch plus one merge launch.  Same results as fl_decode_attn_dense(loop 0) followed by
  * fl_decode_attn_dense(loop 1, logits): logits bit-identical, outputs within float
  * rounding of the partial sums (the split points differ).  No counterpart in the
- * reference, whose step calls dense_source_attention once per loop
- * (flashloop/engine.py:420-436): fusing the two launches pays the end-of-launch
- * imbalance of the persistent grid once.  logits1 is required.
+ * reference, whose decode runs every layer of loop 1 before loop 2
+ * (flashloop/engine.py:393-394), so only a caller holding both loops' queries at once
+ * can use it; one launch pays the persistent grid's end-of-launch imbalance once.
+ * logits1 is required.
  * workspace: fl_decode_attn_dense_pair_workspace() bytes (16-byte aligned, any content).
  */
 size_t fl_decode_attn_dense_pair_workspace(const fl_cache_view* view);

@@ -439,3 +439,30 @@ def test_profile_hook_records_the_dense_reader():
     _lib.check(lib.fl_profile_dense_reader_read(ctypes.byref(tot), ctypes.byref(n)), "read")
     _lib.check(lib.fl_profile_dense_reader(1, 0), "stop")
     assert n.value == 2 and tot.value > 0.0
+
+
+@pytest.mark.parametrize("b,h,t", [(4, 4, 4000), (3, 2, 200), (9, 16, 32768)])
+def test_dense_pair_matches_separate_launches(b, h, t):
+    """fl_decode_attn_dense_pair (loops 1 and 2 in one launch) against the two single-loop
+    launches: loop-2 logits bit-identical; outputs within 2e-3 (the split points of the
+    partial softmax sums differ; each path is held to the oracle by the other tests)."""
+    print("case: dense pair B%d H%d T%d" % (b, h, t), flush=True)
+    w = decode_workload(b, h, t, seed=21, device=DEV)
+    ks = [w.keys[r][:, :, :t].contiguous() for r in range(4)]
+    vs = [w.values[r][:, :, :t].contiguous() for r in range(4)]
+    layer = CrossLoopKVLayer.from_prefill(ks, vs)
+    del ks, vs
+    cur = [w.current(r) for r in range(2)]
+    g = torch.Generator(device="cpu").manual_seed(5)
+    q = [torch.randn(b, h, 1, 128, generator=g).bfloat16().to(DEV) for _ in range(2)]
+    o0, _ = layer.dense_source_attention(0, query=q[0], current_key=cur[0][0], current_value=cur[0][1],
+                                         scaling=SCALING, return_logits=False)
+    o1, lg = layer.dense_source_attention(1, query=q[1], current_key=cur[1][0], current_value=cur[1][1],
+                                          scaling=SCALING, return_logits=True)
+    p0, p1, plg = layer.dense_source_attention_pair(queries=q, current_keys=[c[0] for c in cur],
+                                                    current_values=[c[1] for c in cur], scaling=SCALING)
+    torch.cuda.synchronize()
+    keys = t + 1
+    assert torch.equal(plg[..., :keys], lg[..., :keys])
+    assert (p0 - o0).abs().max().item() < 2e-3
+    assert (p1 - o1).abs().max().item() < 2e-3
