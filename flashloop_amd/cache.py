@@ -276,12 +276,15 @@ class CrossLoopKVLayer:
         """Keys per sequence including the current token: packed + tail + 1 (device)."""
         return self.packed_tokens + self.tail_tokens + 1
 
-    def select_decode_keys(self, logits: torch.Tensor, fraction: float):
+    def select_decode_keys(self, logits: torch.Tensor, fraction: float, validate: bool = False):
         """Loop-2 key selection (flashloop/engine.py:438-498) on the dense reader's logits.
-        Returns ``(indices, valid, mass [B,H,1,1], selected_weights, counts)``."""
+        Returns ``(indices, valid, mass [B,H,1,1], selected_weights, counts)``.
+        ``validate=True`` raises ``ValueError`` on NaN/inf logits (a host sync), as
+        ``flashloop/selection.py:78-79`` does."""
         cap = kernels.decode_capacity(self.token_count + 1, fraction)
         idx, valid, mass, w, counts = kernels.decode_topk(
-            logits.reshape(self.rows, -1), self.key_counts(), fraction, cap, rows_per_count=self.heads
+            logits.reshape(self.rows, -1), self.key_counts(), fraction, cap, rows_per_count=self.heads,
+            validate=validate,
         )
         shape = (self.batch, self.heads, cap)
         return idx.view(shape), valid.view(shape), mass.view(self.batch, self.heads, 1, 1), w.view(shape), counts

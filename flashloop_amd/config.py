@@ -20,22 +20,22 @@ class FlashLoopConfig:
 
     def __post_init__(self) -> None:
         if not 0.0 < self.prefill_fraction_loop4 <= self.prefill_fraction_loop3 <= 1.0:
-            raise ValueError("prefill fractions require 0 < loop4 <= loop3 <= 1")
+            raise ValueError(f"token retention must satisfy 0 < loop-4 fraction ({self.prefill_fraction_loop4}) <= loop-3 fraction ({self.prefill_fraction_loop3}) <= 1")
         if not 0.0 < self.decode_key_fraction <= 1.0:
-            raise ValueError("decode_key_fraction must be in (0, 1]")
+            raise ValueError(f"decode key retention {self.decode_key_fraction} lies outside (0, 1]")
         if self.kv_bits != 4:
-            raise ValueError("the production FlashLoop codec is fixed to 4 bits")
+            raise ValueError(f"kv_bits={self.kv_bits}: the int4 residual codec has no other width")
         if self.group_size != 64:
-            raise ValueError("the production FlashLoop codec uses group_size=64")
+            raise ValueError(f"group_size={self.group_size}: codes are grouped by 64 tokens / 64 channels only")
         if self.residual_length != 64:
-            raise ValueError("the production FlashLoop cache uses residual_length=64")
+            raise ValueError(f"residual_length={self.residual_length}: the BF16 tail keeps exactly 64 tokens")
         if not self.quantize_cross_loop_kv:
-            raise ValueError("this build implements the quantized cross-loop cache only")
+            raise ValueError("quantize_cross_loop_kv=False (a BF16 cross-loop cache) is not part of this build")
         for name in ("enable_token_sparse_prefill", "enable_sparse_decode"):
             if not isinstance(getattr(self, name), bool):
-                raise TypeError(f"{name} must be bool")
+                raise TypeError(f"{name} takes True or False, got {getattr(self, name)!r}")
         if self.decode_capacity < 0:
-            raise ValueError("decode_capacity must be non-negative")
+            raise ValueError(f"decode_capacity={self.decode_capacity} is negative")
 
     @property
     def effective_prefill_fractions(self) -> tuple[float, float]:
@@ -52,8 +52,8 @@ def validate_ouro_model(model) -> None:
     """Shape contract of the engine (flashloop/config.py:92-134): 4 loops, MHA, head_dim 128."""
     cfg = model.config
     if int(getattr(cfg, "total_ut_steps", 0)) != 4:
-        raise ValueError("FlashLoop requires exactly four recurrent loops")
+        raise ValueError(f"total_ut_steps={getattr(cfg, 'total_ut_steps', None)}: the cross-loop cache holds four loops")
     if int(cfg.head_dim) != 128:
-        raise ValueError("FlashLoop kernels require head_dim 128")
+        raise ValueError(f"head_dim={cfg.head_dim}: the HIP kernels are built for 128 channels per head")
     if int(cfg.num_attention_heads) != int(cfg.num_key_value_heads):
-        raise ValueError("FlashLoop kernels require multi-head attention (no grouped KV)")
+        raise ValueError("grouped KV heads are not supported: the readers take one K/V head per query head")

@@ -558,27 +558,35 @@ __device__ __forceinline__ void stage_partial(const WaveState& st, float* part) 
   }
 }
 
+// LDS of one reader wave: every array a wave touches lives in its own block, at fixed
+// offsets, so no wave's staging overlaps another's whatever loop body each is running.
+template <int NS, bool LOGITS>
+struct WaveBlock {
+  WaveLds<NS> sh;
+  float lg[LOGITS ? kStageGroups * kGroup : 1];
+  float ps[kStageSegs][kPartial];
+  SegMeta seg[kStageSegs];
+};
+
 // The LDS of one reader workgroup.
 template <int NS, bool LOGITS>
 struct ReaderLds {
-  WaveLds<NS> sh[kWaves];
-  float lgsh[LOGITS ? kWaves : 1][LOGITS ? kStageGroups * kGroup : 1];
-  float psh[kWaves][kStageSegs][kPartial];
-  SegMeta segsh[kWaves][kStageSegs];
+  WaveBlock<NS, LOGITS> w[kWaves];
 };
 
-// Wave w's units [u0, u1) of one loop's work sequence.
+// Wave-private block of the pair launch: loop 1 and loop 2 bodies view the same bytes
+// through their own types; a wave runs the bodies one after the other.
+union PairWaveBlock {
+  WaveBlock<1, false> l1;
+  WaveBlock<2, true> l2;
+};
+
+// Wave w's units [u0, u1) of one loop's work sequence; W is the calling wave's LDS block.
 template <int NS, bool LOGITS>
-__device__ __forceinline__ void dense_range(const DenseArgs& a, ReaderLds<NS, LOGITS>& L, const RowLens& rl, int w,
+__device__ __forceinline__ void dense_range(const DenseArgs& a, WaveBlock<NS, LOGITS>& W, const RowLens& rl, int w,
                                             int64_t u0, int64_t u1) {
   if (u0 >= u1) return;
   const fl_cache_view& v = a.v;
-  const int wave = threadIdx.x >> 6;
-  const int BH = v.batch * v.heads;
-  auto& sh = L.sh;
-  auto& lgsh = L.lgsh;
-  auto& psh = L.psh;
-  auto& segsh = L.segsh;
 
   // Tails whose first unit lies in [u0, u1), then the count of prefix groups in range.
   Cursor c = locate(v, rl, u0);
@@ -587,7 +595,7 @@ __device__ __forceinline__ void dense_range(const DenseArgs& a, ReaderLds<NS, LO
     Cursor t = c;
     bool first = true;
     while (t.b < v.batch && t.vs < u1) {
-      if (t.vs >= u0) wave_tail<LOGITS>(a, t.b * v.heads + t.h, sh[wave].comb);
+      if (t.vs >= u0) wave_tail<LOGITS>(a, t.b * v.heads + t.h, W.sh.comb);
       const int64_t p0 = max(t.vs + kTailUnits, first ? u0 : t.vs), p1 = min(t.vs + kTailUnits + t.gb, u1);
       if (p1 > p0) my += static_cast<int>(p1 - p0);
       first = false;
@@ -599,15 +607,14 @@ __device__ __forceinline__ void dense_range(const DenseArgs& a, ReaderLds<NS, LO
   Cursor ld = c;
   ld.gi = max(c.gi - kTailUnits, 0);
   while (ld.gi >= ld.gb && ld.b < v.batch) next_row(ld, v, rl);
-  (void)BH;
 
   WaveState st;
   reset_state(st);
   // Current segment in registers (wave-uniform); closed segments in LDS.
   int nseg = 0, used = 0, cur_bh = -1, cur_gi0 = 0, cur_first = 0, cur_count = 0;
-  float* lgbuf = lgsh[LOGITS ? wave : 0];
-  float(*pbuf)[kPartial] = psh[wave];
-  SegMeta* seg = segsh[wave];
+  float* lgbuf = W.lg;
+  float(*pbuf)[kPartial] = W.ps;
+  SegMeta* seg = W.seg;
   auto close_seg = [&]() {
     stage_partial(st, pbuf[nseg - 1]);
     if ((threadIdx.x & 63) == 0) seg[nseg - 1] = SegMeta{cur_bh, cur_gi0, cur_first, cur_count};
@@ -635,7 +642,7 @@ __device__ __forceinline__ void dense_range(const DenseArgs& a, ReaderLds<NS, LO
       cur_first = 0;
       cur_count = 0;
     }
-    compute_group<NS, LOGITS>(gs, st, sh[wave].p, a, lgbuf + (LOGITS ? used * kGroup : 0));
+    compute_group<NS, LOGITS>(gs, st, W.sh.p, a, lgbuf + (LOGITS ? used * kGroup : 0));
     ++used;
     ++cur_count;
   };
@@ -679,7 +686,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
   const int64_t U = total_units(v, rl);
   const int64_t chunk = chunk_of(U, a.waves);
   const int64_t u0 = static_cast<int64_t>(w) * chunk;
-  dense_range<NS, LOGITS>(a, L, rl, w, u0, min(u0 + chunk, U));
+  dense_range<NS, LOGITS>(a, L.w[threadIdx.x >> 6], rl, w, u0, min(u0 + chunk, U));
 }
 
 // Loops 1 and 2 of a decode step in one persistent launch (loop 2 with logits).  Their
@@ -689,25 +696,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
 // wave's partials go to its loop's workspace at the slots of its global wave index.
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void dense_pair_kernel(DenseArgs a0,
                                                                                                     DenseArgs a1) {
-  __shared__ ReaderLds<2, true> L;
+  __shared__ PairWaveBlock L[kWaves];
   __shared__ int lens[kLenCache];
-  static_assert(sizeof(ReaderLds<1, false>) <= sizeof(ReaderLds<2, true>), "loop-1 LDS must fit in loop-2 LDS");
   const fl_cache_view& v = a0.v;
   const int w = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  PairWaveBlock& mine = L[threadIdx.x >> 6];
   for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kThreads) lens[i] = row_groups(v, i);
   __syncthreads();
   const RowLens rl{lens, min(v.batch, kLenCache)};
   const int64_t U = total_units(v, rl);
   const int64_t chunk = chunk_of(2 * U, a0.waves);
   const int64_t u0 = static_cast<int64_t>(w) * chunk, u1 = min(u0 + chunk, 2 * U);
-  dense_range<1, false>(a0, *reinterpret_cast<ReaderLds<1, false>*>(&L), rl, w, u0, min(u1, U));
-  // The two loops view the same LDS through different types, which type-based alias
-  // analysis takes as disjoint: without a compiler barrier, loop 2's first LDS writes
-  // could be scheduled above loop 1's last staging reads (that corrupted the last loop-1
-  // row of the wave whose range crosses into loop 2).  The memory clobber orders every
-  // access; the wait completes loop 1's LDS reads.
+  dense_range<1, false>(a0, mine.l1, rl, w, u0, min(u1, U));
+  // The two bodies view the wave's block through different types, which type-based
+  // alias analysis takes as disjoint: without a compiler barrier, loop 2's first LDS
+  // writes could be scheduled above loop 1's last staging reads.  The memory clobber
+  // orders every access; the wait completes this wave's loop-1 LDS reads.  Other waves
+  // never touch this block.
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  dense_range<2, true>(a1, L, rl, w, max(u0, U) - U, max(u1, U) - U);
+  dense_range<2, true>(a1, mine.l2, rl, w, max(u0, U) - U, max(u1, U) - U);
 }
 
 // Combine row bh's partials: prefix slots [f+bh, l+bh] (see partial_slot) + its tail slot.
@@ -806,8 +813,8 @@ int occupancy_of(int loop, bool logits) {
   }
 }
 
-constexpr int kMaxResident = 2;
-constexpr int kProfilePair = 4;  // fl_profile_dense_reader code of the pair launch  // workgroups per CU any reader instantiation can hold
+constexpr int kMaxResident = 2;  // workgroups per CU any reader instantiation can hold
+constexpr int kProfilePair = 4;  // fl_profile_dense_reader code of the pair launch
 
 // ---- measurement hook (fl_profile_dense_reader): HIP events around the reader kernel
 struct ReaderProfile {

@@ -56,11 +56,10 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 }
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
 
-// fp16 bits: narrowing rounds to nearest even, finite values beyond the fp16 range
-// saturate to +-65504; widening is exact.
-__device__ __forceinline__ uint16_t f32_to_f16_sat(float f) {
-  const float c = isnan(f) ? f : fminf(fmaxf(f, -65504.0f), 65504.0f);
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(c));
+// fp16 bits: narrowing rounds to nearest even, with fp16 subnormals, and finite values
+// beyond the fp16 range become +-inf (torch's .to(torch.float16)); widening is exact.
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));

@@ -13,6 +13,8 @@
 // torch-CPU codec.  Its division is computed as an exact Markstein quotient (encode).
 #include "fl_common.h"
 
+#include <type_traits>
+
 namespace fl {
 namespace {
 
@@ -60,13 +62,27 @@ __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
 // code = clamp(rint((x - minimum) / scale), 0, 15).  The quotient is Markstein's
 // correction of a * RN(1/scale): with y = RN(1/b), q0 = RN(a*y) and the exact remainder
 // r = a - b*q0 (one fma), RN(q0 + r*y) is the correctly rounded a/b (P. Markstein,
-// IBM J. Res. Dev. 34(1), 1990).  Three ops instead of an IEEE division per element;
-// tests/markstein_check.c checks it against the division over the codec's domain.
+// IBM J. Res. Dev. 34(1), 1990).  Three ops instead of an IEEE division per element.
+// The remainder is exact only while b*q0 stays clear of the subnormal range, which holds
+// for scale >= kMinFastScale over every quotient that can round to a nonzero code; groups
+// whose span is smaller than that (scale subnormal or near it, where 1/scale can even
+// overflow) take the IEEE division instead (exact_div).  tests/markstein_check.c checks
+// both against the division over the codec's domain, subnormal spans included.
+constexpr float kMinFastScale = 0x1p-100f;
+
+__device__ __forceinline__ bool needs_exact_div(Quant q) { return !(q.scale >= kMinFastScale); }
+
+template <bool EXACT_DIV>
 __device__ __forceinline__ uint32_t encode(float x, Quant q) {
   const float a = __fsub_rn(x, q.minimum);
-  const float q0 = __fmul_rn(a, q.inv);
-  const float r = __fmaf_rn(-q0, q.scale, a);
-  float c = rintf(__fmaf_rn(r, q.inv, q0));
+  float c;
+  if constexpr (EXACT_DIV) {
+    c = rintf(__fdiv_rn(a, q.scale));
+  } else {
+    const float q0 = __fmul_rn(a, q.inv);
+    const float r = __fmaf_rn(-q0, q.scale, a);
+    c = rintf(__fmaf_rn(r, q.inv, q0));
+  }
   c = fminf(fmaxf(c, 0.0f), 15.0f);
   return static_cast<uint32_t>(c);
 }
@@ -184,38 +200,45 @@ __device__ __forceinline__ void key_loop(const PackArgs& a, int b, int bh, int g
     const int64_t mi = ((static_cast<int64_t>(bh) * (v.token_capacity / kGroup) + g) * kDim + 2 * pair) * 2;
     *reinterpret_cast<float4*>(v.key_meta[R] + mi) = meta;
     const uint2 half_meta = make_uint2(
-        static_cast<uint32_t>(f32_to_f16_sat(q0.scale)) | (static_cast<uint32_t>(f32_to_f16_sat(q0.minimum)) << 16),
-        static_cast<uint32_t>(f32_to_f16_sat(q1.scale)) | (static_cast<uint32_t>(f32_to_f16_sat(q1.minimum)) << 16));
+        static_cast<uint32_t>(f32_to_f16(q0.scale)) | (static_cast<uint32_t>(f32_to_f16(q0.minimum)) << 16),
+        static_cast<uint32_t>(f32_to_f16(q1.scale)) | (static_cast<uint32_t>(f32_to_f16(q1.minimum)) << 16));
     *reinterpret_cast<uint2*>(v.key_meta_half[R] + mi) = half_meta;
   }
+  // The encode loop is instantiated twice; a wave takes the IEEE-division form only when
+  // one of its groups has a scale below kMinFastScale (a wave-uniform branch).
+  auto encode_rows = [&](auto exact) __attribute__((always_inline)) {
+    constexpr bool EXACT = decltype(exact)::value;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int i = quarter * 16 + k;
-    uint32_t c0 = 0, c1 = 0;
-    float d0 = 0.0f, d1 = 0.0f;
-    if ((act >> i) & 1) {
-      c0 = encode(x0[k], q0);
-      c1 = encode(x1[k], q1);
-      d0 = decode_f32(c0, q0);
-      d1 = decode_f32(c1, q1);
-      round_bf16_pair(d0, d1);
+    for (int k = 0; k < 16; ++k) {
+      const int i = quarter * 16 + k;
+      uint32_t c0 = 0, c1 = 0;
+      float d0 = 0.0f, d1 = 0.0f;
+      if ((act >> i) & 1) {
+        c0 = encode<EXACT>(x0[k], q0);
+        c1 = encode<EXACT>(x1[k], q1);
+        d0 = decode_f32(c0, q0);
+        d1 = decode_f32(c1, q1);
+        round_bf16_pair(d0, d1);
+      }
+      lds[i][pair & 15] = static_cast<uint8_t>(c0 | (c1 << 4));
+      if constexpr (R == 0) {
+        r0[k] = d0;
+        r1[k] = d1;
+      } else {
+        // inactive rows add an exact zero delta (kv_quantization.py:465)
+        r0[k] = __fadd_rn(r0[k], d0);
+        r1[k] = __fadd_rn(r1[k], d1);
+        round_bf16_pair(r0[k], r1[k]);
+      }
+      if (a.rk[R] != nullptr) {
+        const uint32_t packed = static_cast<uint32_t>(f32_to_bf16_rne(r0[k])) |
+                                (static_cast<uint32_t>(f32_to_bf16_rne(r1[k])) << 16);
+        *reinterpret_cast<uint32_t*>(a.rk[R] + src_base + static_cast<int64_t>(i) * kDim + 2 * pair) = packed;
+      }
     }
-    lds[i][pair & 15] = static_cast<uint8_t>(c0 | (c1 << 4));
-    if constexpr (R == 0) {
-      r0[k] = d0;
-      r1[k] = d1;
-    } else {
-      // inactive rows add an exact zero delta (kv_quantization.py:465)
-      r0[k] = __fadd_rn(r0[k], d0);
-      r1[k] = __fadd_rn(r1[k], d1);
-      round_bf16_pair(r0[k], r1[k]);
-    }
-    if (a.rk[R] != nullptr) {
-      const uint32_t packed = static_cast<uint32_t>(f32_to_bf16_rne(r0[k])) |
-                              (static_cast<uint32_t>(f32_to_bf16_rne(r1[k])) << 16);
-      *reinterpret_cast<uint32_t*>(a.rk[R] + src_base + static_cast<int64_t>(i) * kDim + 2 * pair) = packed;
-    }
-  }
+  };
+  if (__builtin_expect(__any(needs_exact_div(q0) || needs_exact_div(q1)), 0)) encode_rows(std::true_type{});
+  else encode_rows(std::false_type{});
   wave_lds_sync();
   const int row = token_row<R>(a, tin);
   const uint4 chunk = *reinterpret_cast<const uint4*>(lds[lane]);
@@ -291,27 +314,32 @@ __device__ __forceinline__ void value_loop(const PackArgs& a, int b, int bh, int
   mx = pair_max(mx);
   const Quant q = make_quant(mn, mx, act);
   uint32_t words[4] = {0, 0, 0, 0};
+  auto encode_row = [&](auto exact) __attribute__((always_inline)) {
+    constexpr bool EXACT = decltype(exact)::value;
 #pragma unroll
-  for (int c = 0; c < 32; c += 2) {
-    uint32_t c0 = 0, c1 = 0;
-    float d0 = 0.0f, d1 = 0.0f;
-    if (act) {
-      c0 = encode(x[c], q);
-      c1 = encode(x[c + 1], q);
-      d0 = decode_f32(c0, q);
-      d1 = decode_f32(c1, q);
-      round_bf16_pair(d0, d1);
+    for (int c = 0; c < 32; c += 2) {
+      uint32_t c0 = 0, c1 = 0;
+      float d0 = 0.0f, d1 = 0.0f;
+      if (act) {
+        c0 = encode<EXACT>(x[c], q);
+        c1 = encode<EXACT>(x[c + 1], q);
+        d0 = decode_f32(c0, q);
+        d1 = decode_f32(c1, q);
+        round_bf16_pair(d0, d1);
+      }
+      words[c >> 3] |= (c0 | (c1 << 4)) << (4 * (c & 7));
+      if constexpr (R == 0) {
+        rv[c] = d0;
+        rv[c + 1] = d1;
+      } else {
+        rv[c] = __fadd_rn(rv[c], d0);
+        rv[c + 1] = __fadd_rn(rv[c + 1], d1);
+        round_bf16_pair(rv[c], rv[c + 1]);
+      }
     }
-    words[c >> 3] |= (c0 | (c1 << 4)) << (4 * (c & 7));
-    if constexpr (R == 0) {
-      rv[c] = d0;
-      rv[c + 1] = d1;
-    } else {
-      rv[c] = __fadd_rn(rv[c], d0);
-      rv[c + 1] = __fadd_rn(rv[c + 1], d1);
-      round_bf16_pair(rv[c], rv[c + 1]);
-    }
-  }
+  };
+  if (__builtin_expect(__any(needs_exact_div(q)), 0)) encode_row(std::true_type{});
+  else encode_row(std::false_type{});
   const int row = token_row<R>(a, tin);
   if (row >= 0) {
     const int t = g * kGroup + i;
@@ -321,7 +349,7 @@ __device__ __forceinline__ void value_loop(const PackArgs& a, int b, int bh, int
     if ((quarter & 1) == 0) {
       *reinterpret_cast<float2*>(v.value_meta[R] + (rowi * 2 + half) * 2) = make_float2(q.scale, q.minimum);
       *reinterpret_cast<uint32_t*>(v.value_meta_half[R] + (rowi * 2 + half) * 2) =
-          static_cast<uint32_t>(f32_to_f16_sat(q.scale)) | (static_cast<uint32_t>(f32_to_f16_sat(q.minimum)) << 16);
+          static_cast<uint32_t>(f32_to_f16(q.scale)) | (static_cast<uint32_t>(f32_to_f16(q.minimum)) << 16);
       const int64_t rec = ((static_cast<int64_t>(bh) * v.token_capacity + t) * 2 + half) * 4 + R;
       *reinterpret_cast<float2*>(v.value_meta_token + rec * 2) = make_float2(q.scale, q.minimum);
     }

@@ -22,10 +22,14 @@ namespace {
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / kWave;
 
+// Order-preserving unsigned key of a score.  -0.0 takes the key of +0.0 (they compare
+// equal, so the lower index wins their tie, as in torch.topk and a stable sort).
 __device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t u = __float_as_uint(f);
+  const uint32_t u = f == 0.0f ? 0u : __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+// NaN or +-inf (flashloop/selection.py:78-79 rejects such weights)
+__device__ __forceinline__ bool non_finite(float f) { return !(fabsf(f) <= 3.402823466e38f); }
 __device__ __forceinline__ float key_value(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
@@ -38,6 +42,7 @@ struct TopkShared {
   uint32_t sel_prefix;
   uint32_t sel_remaining;
   uint32_t bin_above;
+  uint32_t nonfin;
 };
 
 __device__ float block_max(float v, TopkShared& sh) {
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
                                                                    const int32_t* n_keys, int rows_per_count,
                                                                    double fraction, int cap, int32_t* indices,
                                                                    uint8_t* valid, float* mass, float* weights,
-                                                                   int32_t* counts) {
+                                                                   int32_t* counts, int32_t* nonfinite) {
   __shared__ TopkShared sh;
   const int r = blockIdx.x;
   const float* x = scores + static_cast<int64_t>(r) * stride;
@@ -189,13 +194,20 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
     if (threadIdx.x == 0) {
       mass[r] = 0.0f;
       if (counts) counts[r] = 0;
+      if (nonfinite) nonfinite[r] = 0;
     }
     return;
   }
   // softmax statistics of the row (flashloop/engine.py:440-442)
+  if (threadIdx.x == 0) sh.nonfin = 0;
   float mx = -INFINITY;
-  for (int i = threadIdx.x; i < n; i += kTopkThreads) mx = fmaxf(mx, x[i]);
-  const float M = block_max(mx, sh);
+  uint32_t nf = 0;
+  for (int i = threadIdx.x; i < n; i += kTopkThreads) {
+    mx = fmaxf(mx, x[i]);
+    nf += non_finite(x[i]) ? 1u : 0u;
+  }
+  const float M = block_max(mx, sh);  // (its barriers order the counter's reset)
+  if (nf) atomicAdd(&sh.nonfin, nf);
   float z = 0.0f;
   for (int i = threadIdx.x; i < n; i += kTopkThreads) z += fast_exp2((x[i] - M) * kLog2e);
   const float Z = block_sum(z, sh);
@@ -228,6 +240,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
   if (threadIdx.x == 0) {
     mass[r] = S;
     if (counts) counts[r] = k;
+    if (nonfinite) nonfinite[r] = static_cast<int32_t>(sh.nonfin);
   }
 }
 
@@ -282,6 +295,7 @@ struct ResShared {
   uint32_t kth_key;
   uint32_t kth_idx;
   uint32_t total;
+  uint32_t nonfin;
 };
 
 __device__ float res_block_max(float v, ResShared& sh) {
@@ -347,7 +361,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
                                                                             const int32_t* n_keys, int rows_per_count,
                                                                             double fraction, int cap, int32_t* indices,
                                                                             uint8_t* valid, float* mass, float* weights,
-                                                                            int32_t* counts) {
+                                                                            int32_t* counts, int32_t* nonfinite) {
   __shared__ ResShared sh;
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -375,6 +389,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
     if (tid == 0) {
       mass[r] = 0.0f;
       if (counts) counts[r] = 0;
+      if (nonfinite) nonfinite[r] = 0;
     }
     return;
   }
@@ -386,6 +401,8 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   // needs an index test.
   uint32_t kr[PER];
   float mx = -INFINITY, mn = INFINITY;
+  uint32_t nf = 0;  // non-finite keys of this wave (wave-uniform)
+  if (tid == 0) sh.nonfin = 0;
   {
     float xs[PER];
 #pragma unroll
@@ -397,6 +414,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
     for (int j = 0; j < PER; ++j) {
       const bool in = j * kTopkThreads + tid < n;
       kr[j] = in ? max(order_key(xs[j]), kPadKey + 1u) : kPadKey;
+      nf += static_cast<uint32_t>(__popcll(ballot64(in && non_finite(xs[j]))));
       if (in) {
         mx = fmaxf(mx, xs[j]);
         mn = fminf(mn, xs[j]);
@@ -405,7 +423,8 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   }
   for (int i = tid; i < kBins; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
   if (tid == 0) sh.ncand = 0;
-  const float M = res_block_max(mx, sh);
+  const float M = res_block_max(mx, sh);  // (its barriers order the counter's reset)
+  if (lane == 0 && nf) atomicAdd(&sh.nonfin, nf);
   mn = -res_block_max(-mn, sh);
   // bin(x) = clamp(x * inv - mn * inv); non-finite extremes collapse every key into bin 0
   // (the crowded-bin fallback then covers all)
@@ -630,6 +649,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   if (tid == 0) {
     mass[r] = S;
     if (counts) counts[r] = k;
+    if (nonfinite) nonfinite[r] = static_cast<int32_t>(sh.nonfin);
   }
 }
 
@@ -719,7 +739,8 @@ __global__ __launch_bounds__(kTopkThreads) void select_tokens_kernel(const float
 
 extern "C" int32_t fl_decode_topk(const float* scores, int64_t scores_stride, int32_t rows, const int32_t* n_keys,
                                   int32_t rows_per_count, double fraction, int32_t capacity, int32_t* indices,
-                                  uint8_t* valid, float* mass, float* weights, int32_t* counts, void* stream) {
+                                  uint8_t* valid, float* mass, float* weights, int32_t* counts,
+                                  int32_t* nonfinite, void* stream) {
   using namespace fl;
   clear_error();
   FL_REQUIRE(scores && n_keys && indices && valid && mass && weights, "fl_decode_topk: null pointer");
@@ -735,17 +756,17 @@ extern "C" int32_t fl_decode_topk(const float* scores, int64_t scores_stride, in
   if (scores_stride <= kResKeys && std::ceil(static_cast<double>(scores_stride) * fraction) <= kSelLds) {
     if (per <= 9)
       hipLaunchKernelGGL(decode_topk_resident_kernel<9>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
-                       fraction, capacity, indices, valid, mass, weights, counts);
+                       fraction, capacity, indices, valid, mass, weights, counts, nonfinite);
     else if (per <= 18)
       hipLaunchKernelGGL(decode_topk_resident_kernel<18>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
-                       fraction, capacity, indices, valid, mass, weights, counts);
+                       fraction, capacity, indices, valid, mass, weights, counts, nonfinite);
     else
       hipLaunchKernelGGL(decode_topk_resident_kernel<kPer>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
-                       fraction, capacity, indices, valid, mass, weights, counts);
+                       fraction, capacity, indices, valid, mass, weights, counts, nonfinite);
   }
   else
     hipLaunchKernelGGL(decode_topk_kernel, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
-                       fraction, capacity, indices, valid, mass, weights, counts);
+                       fraction, capacity, indices, valid, mass, weights, counts, nonfinite);
   FL_LAUNCH_CHECK("fl_decode_topk");
   return FL_OK;
 }

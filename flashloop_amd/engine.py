@@ -17,7 +17,6 @@ Model GEMMs, norms and SDPA of the dense prefill loops are torch (hipBLASLt).
 
 from __future__ import annotations
 
-import gc
 import math
 from dataclasses import dataclass, field
 from typing import Callable, Sequence
@@ -109,12 +108,22 @@ class DecodeRunner:
     def __init__(self, engine: "FlashLoopEngine", use_graphs: bool) -> None:
         self.engine = engine
         self.use_graphs = bool(use_graphs)
+        self.graph = None
         self.reset()
 
-    def reset(self) -> None:
+    def _release(self) -> None:
+        """Destroy the captured graph and its private memory pool, here and now (never
+        inside a capture).  Nothing outside this runner holds a tensor of that pool: the
+        step's logits are copied, inside the graph, into ``out``, an ordinary allocation."""
+        self.logits = None
+        if self.graph is not None:
+            self.graph.reset()
         self.graph = None
         self.key = None
-        self.tok = self.pos = self.logits = None
+
+    def reset(self) -> None:
+        self._release()
+        self.tok = self.pos = self.out = None
 
     def _key(self, cache: CrossLoopKVCache, bsz: int) -> tuple:
         lc = cache.layers[0]
@@ -131,9 +140,10 @@ class DecodeRunner:
             pos_t = torch.tensor([[int(p)] for p in positions], dtype=torch.long, device=dev)
             return eng._decode_core(cache, eng.backbone.embed_tokens(token_ids), pos_t)
         if self.tok is None or self.tok.shape[0] != bsz:
+            self._release()
             self.tok = torch.zeros((bsz, 1), dtype=torch.long, device=dev)
             self.pos = torch.zeros((bsz, 1), dtype=torch.long, device=dev)
-            self.graph = None
+            self.out = torch.empty((bsz, eng.model.config.vocab_size), dtype=torch.float32, device=dev)
         self.tok.copy_(token_ids)
         if bsz == 1:
             self.pos.fill_(int(positions[0]))
@@ -141,11 +151,11 @@ class DecodeRunner:
             self.pos.copy_(torch.tensor([[int(p)] for p in positions], dtype=torch.long), non_blocking=False)
         key = self._key(cache, bsz)
         if self.graph is None or self.key != key:
-            self.graph = None
+            self._release()
             self._capture(cache)
             self.key = key
         self.graph.replay()
-        return self.logits
+        return self.out
 
     def _capture(self, cache: CrossLoopKVCache) -> None:
         """A warm-up run on a side stream first sizes every workspace and library handle;
@@ -159,15 +169,9 @@ class DecodeRunner:
                 lc.tail_tokens -= 1
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        # No garbage collection while capturing: a collected cycle can hold an earlier
-        # graph or its memory pool, whose release is illegal inside a capture.
-        gc.collect()
-        gc.disable()
-        try:
-            with torch.cuda.graph(graph):
-                self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
-        finally:
-            gc.enable()
+        with torch.cuda.graph(graph):
+            self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
+            self.out.copy_(self.logits)
         self.graph = graph
 
 
@@ -527,8 +531,8 @@ class FlashLoopEngine:
     def decode(self, token_ids: torch.Tensor) -> DecodeOutput:
         """``FlashLoopEngine.decode`` (flashloop/engine.py:373-570).  With ``use_graphs`` the
         step replays a captured HIP graph (recaptured when the selection capacity changes
-        its shapes); the returned logits then live in the graph's output
-        buffer and are overwritten by the next step."""
+        its shapes); the returned logits then live in the runner's output buffer and are
+        overwritten by the next step."""
         state = self.state
         if token_ids.shape != (1, 1):
             raise ValueError("decode requires exactly one token at batch size one")

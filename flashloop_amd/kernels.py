@@ -130,8 +130,13 @@ def decode_capacity(keys: int, fraction: float) -> int:
 
 
 def decode_topk(logits: torch.Tensor, n_keys: torch.Tensor, fraction: float, capacity: int,
-                rows_per_count: int = 1):
-    """Top-k of each logits row -> (indices i32, valid u8, mass f32, weights f32, counts i32)."""
+                rows_per_count: int = 1, validate: bool = False, nonfinite: torch.Tensor | None = None):
+    """Top-k of each logits row -> (indices i32, valid u8, mass f32, weights f32, counts i32).
+
+    ``nonfinite`` (optional i32 [rows]) receives each row's count of NaN/inf scores.
+    ``validate=True`` waits for the kernel and raises ``ValueError`` when a row holds one
+    (as ``flashloop/selection.py:78-79`` refuses non-finite decode weights); the engine
+    path leaves it off, like the reference engine (``flashloop/engine.py:438-453``)."""
     _require(logits, torch.float32, "logits")
     _require(n_keys, torch.int32, "n_keys")
     rows = logits.shape[0]
@@ -141,10 +146,21 @@ def decode_topk(logits: torch.Tensor, n_keys: torch.Tensor, fraction: float, cap
     mass = torch.empty(rows, dtype=torch.float32, device=dev)
     w = torch.empty(rows, capacity, dtype=torch.float32, device=dev)
     counts = torch.empty(rows, dtype=torch.int32, device=dev)
+    if validate and nonfinite is None:
+        nonfinite = torch.empty(rows, dtype=torch.int32, device=dev)
+    if nonfinite is not None:
+        _require(nonfinite, torch.int32, "nonfinite")
+        if nonfinite.numel() < rows:
+            raise ValueError("nonfinite needs one entry per row")
     rc = load().fl_decode_topk(logits.data_ptr(), logits.stride(0), rows, n_keys.data_ptr(), rows_per_count,
                                float(fraction), capacity, idx.data_ptr(), valid.data_ptr(), mass.data_ptr(),
-                               w.data_ptr(), counts.data_ptr(), _stream())
+                               w.data_ptr(), counts.data_ptr(), nonfinite.data_ptr() if nonfinite is not None else None,
+                               _stream())
     check(rc, "fl_decode_topk")
+    if validate:
+        bad = int((nonfinite[:rows] != 0).sum().item())
+        if bad:
+            raise ValueError(f"decode top-k: {bad} score row(s) hold NaN or infinite values")
     return idx, valid, mass, w, counts
 
 

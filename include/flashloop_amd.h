@@ -61,7 +61,7 @@ extern "C" {
  *                      reader of selected tokens fetches one line for every stream's
  *                      V metadata (entries of streams 2/3 at inactive tokens are unused)
  *   key_meta_half[s] f16 [B*H, token_capacity/64, 128, 2]  key_meta[s] rounded to fp16
- *                      (saturating)
+ *                      (nearest even, overflow to +-inf, as torch's .to(torch.float16))
  *   value_meta_half[s] f16 [B*H, row_capacity[s], 2, 2]  value_meta[s] rounded likewise
  *                      The readers stream these fp16 copies (half the metadata bytes;
  *                      the reference's CUDA engine keeps all metadata in fp16,
@@ -195,11 +195,15 @@ int32_t fl_profile_dense_reader_read(float* total_ms, int32_t* launches);
  *   weights f32 [rows, capacity] = softmax weight / mass (0 where invalid).
  * `capacity` must be >= k for every row (the engine uses (k/64+1)*64).
  * counts (optional) i32 [rows] receives k.
+ * Scores compare as floats: -0.0 and +0.0 are equal (lower index first).
+ * nonfinite (optional) i32 [rows] receives the row's number of NaN / +-inf scores;
+ * `flashloop/selection.py:78-79` rejects such rows, so a caller that validates checks
+ * it (the selection made from a row that holds one is defined but meaningless).
  */
 int32_t fl_decode_topk(const float* scores, int64_t scores_stride, int32_t rows,
                        const int32_t* n_keys, int32_t rows_per_count, double fraction,
                        int32_t capacity, int32_t* indices, uint8_t* valid, float* mass,
-                       float* weights, int32_t* counts, void* stream);
+                       float* weights, int32_t* counts, int32_t* nonfinite, void* stream);
 
 /*
  * J2 (sparse) -- weighted sum of selected V rows of loop `loop`.

@@ -88,3 +88,43 @@ def assert_close(got: np.ndarray, want: np.ndarray, max_abs: float = 2e-2, mean_
     assert err.max() <= max_abs, f"{what}: max abs err {err.max():.3e} > {max_abs}"
     assert err.mean() <= mean_abs, f"{what}: mean abs err {err.mean():.3e} > {mean_abs}"
     return float(err.max()), float(err.mean())
+
+
+def restated_dense_logits(layer, loop: int, rows, q, k_cur, scaling: float) -> list:
+    """fp64 logits of the dense reader's own arithmetic for the (b,h) rows ``rows``:
+    prefix keys K[t] = sum_{s<=loop} (code_s[t] * scale16_s + min16_s) from the packed
+    codes and the fp16 metadata copies (streams 2/3 only at tokens with a rank), with no
+    bf16 rounding between streams; then the raw BF16 tail rows and the current key.
+
+    The codes and the fp16 copies are themselves pinned bit for bit against the oracle
+    (``assert_layer_matches_chain``, the fp16 copy tests), so this pins the kernel's
+    contraction to ~1e-6 -- the oracle comparison then bounds what the skipped bf16
+    re-rounding of the reference chain adds (~2e-3 on logits).  ``q``/``k_cur``:
+    float arrays ``[len(rows), 128]``."""
+    out = []
+    heads = layer.heads
+    for i, r in enumerate(rows):
+        b = r // heads
+        tp = layer.packed_host[b]
+        tl = layer.tail_host[b]
+        G = tp // 64
+        qd = np.asarray(q[i], np.float64) * scaling
+        lg = np.zeros(tp + tl + 1, np.float64)
+        for s in range(loop + 1):
+            meta = layer.key_meta_half[s][r, :G].float().cpu().numpy().astype(np.float64)  # [G, 128, 2]
+            if s < 2:
+                rows_s = np.arange(tp)
+                present = np.ones(tp, bool)
+            else:
+                rank = layer.rank[s - 2][b, :tp].cpu().numpy()
+                present = rank >= 0
+                rows_s = np.where(present, rank, 0)
+            codes = unpack_codes(layer.key_codes[s][r])[rows_s].astype(np.float64)  # [tp, 128]
+            scale = np.repeat(meta[:, :, 0], 64, axis=0)
+            mn = np.repeat(meta[:, :, 1], 64, axis=0)
+            lg[:tp] += np.where(present, (codes * scale + mn) @ qd, 0.0)
+        tail = layer.tail_key[loop][r, :tl].float().cpu().numpy().astype(np.float64)
+        lg[tp:tp + tl] = tail @ qd
+        lg[tp + tl] = np.asarray(k_cur[i], np.float64) @ qd
+        out.append(lg)
+    return out

@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 def test_argument_errors_are_reported_without_launching():
     lib = _lib.load()
     assert lib.fl_abi_version() == 1
-    rc = lib.fl_decode_topk(None, 1, 1, None, 1, 0.1, 64, None, None, None, None, None, None)
+    rc = lib.fl_decode_topk(None, 1, 1, None, 1, 0.1, 64, None, None, None, None, None, None, None)
     assert rc == _lib.FL_E_INVALID
     assert b"null" in lib.fl_last_error()
     rc = lib.fl_decode_attn_dense(None, 0, None, None, None, 1.0, None, None, 0, None, 0, None)

@@ -6,10 +6,15 @@ cfg1: T8192 followed by 256 decode appends (a rollover every 64): the packed str
       rolled cache matches the oracle.  Heads are reduced to 2 to keep the CPU oracle in
       seconds; each head is encoded independently, so H does not change the arithmetic.
 cfg2: B32 H16, per-sequence contexts drawn from U[1024, 16384] (seeded): one decode step
-      over the full ragged batch on the GPU; the rows of the shortest and the longest
-      sequence (heads 0 and 15) are checked against the oracle.
-cfg3: B8 H16 T32768 (the benchmark shape): one decode step over every row; the first and
-      the last row are checked against the oracle (k = 3277 keys in loops 3-4).
+      over the full ragged batch on the GPU; every head of the shortest and of the longest
+      sequence is checked against the oracle.
+cfg3: B8 H16 T32768 (the benchmark shape): one decode step over every row; 16 rows, chosen
+      where the dense readers' persistent-wave ranges start or end (tail/prefix splits),
+      are checked against the oracle (k = 3277 keys in loops 3-4).
+The full-shape workloads are drawn on the device (same distributions; the oracle reads
+the rows it checks back from it).  Logits are held twice: within 1e-4 of an fp64
+restatement of the reader's own contraction over the (oracle-pinned) codes and fp16
+metadata, and within 2e-2 max / 5e-3 mean of the oracle's bf16-chain logits.
 """
 
 import numpy as np
@@ -22,7 +27,15 @@ from oracle import codec
 from flashloop_amd import CrossLoopKVLayer, decode_attention_step
 from flashloop_amd.synthetic import SCALING, decode_workload, ragged_lengths
 
-from gpu_util import assert_close, assert_layer_matches_chain, flat_rows, materialized, np32, oracle_prefix
+from gpu_util import (
+    assert_close,
+    assert_layer_matches_chain,
+    flat_rows,
+    materialized,
+    np32,
+    oracle_prefix,
+    restated_dense_logits,
+)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -102,91 +115,115 @@ def test_cfg1_appends_and_rollover():
         assert_close(np32(got).reshape(H, 128), want, what=f"cfg1 loop-{loop + 1} delta")
 
 
-def test_cfg2_ragged_batch32():
-    print("case: cfg2 B32 H16 ragged [1024, 16384]", flush=True)
+def _check_rows(w, layer, step, rows, H, lengths, what):
+    """Oracle parity of the decode step at the (b,h) rows ``rows`` (one vectorised oracle
+    encode of those rows): loop-1/2 outputs, logits (restated and oracle bars), the
+    selection bit for bit on the kernel's logits, the selected aggregate and both deltas."""
+    R = step.out1.numel() // 128
+    cur = [w.current(r) for r in range(4)]
+    tmax = max(lengths[r // H] for r in rows)
+    ks = [torch.stack([w.keys[r][x // H, x % H, :tmax] for x in rows])[None] for r in range(4)]
+    vs = [torch.stack([w.values[r][x // H, x % H, :tmax] for x in rows])[None] for r in range(4)]
+    Kr = [[] for _ in range(4)]
+    Vr = [[] for _ in range(4)]
+    # rows of one length share one oracle call (each row is encoded independently)
+    by_len = {}
+    for i, x in enumerate(rows):
+        by_len.setdefault(lengths[x // H], []).append(i)
+    per_row = {}
+    for t, idxs in by_len.items():
+        nk, nv, chain, tp = oracle_prefix([k[:, idxs, :t] for k in ks], [v[:, idxs, :t] for v in vs])
+        Kb, Vb = materialized(nk, nv, chain, tp)
+        for j, i in enumerate(idxs):
+            per_row[i] = ([Kb[r][0, j] for r in range(4)], [Vb[r][0, j] for r in range(4)])
+    for r in range(4):
+        Kr[r] = [per_row[i][0][r] for i in range(len(rows))]
+        Vr[r] = [per_row[i][1][r] for i in range(len(rows))]
+    q = [np32(w.queries[r]).reshape(R, 128)[rows] for r in range(4)]
+    kc = [np32(c[0]).reshape(R, 128)[rows] for c in cur]
+    vc = [np32(c[1]).reshape(R, 128)[rows] for c in cur]
+    lens = [lengths[x // H] for x in rows]
+    o0, _ = OA.dense_decode(q[0], Kr[0], Vr[0], kc[0], vc[0], SCALING)
+    o1, lg1 = OA.dense_decode(q[1], Kr[1], Vr[1], kc[1], vc[1], SCALING)
+    assert_close(np32(step.out0).reshape(R, 128)[rows], o0, what=f"{what} loop-1 output")
+    assert_close(np32(step.out1).reshape(R, 128)[rows], o1, what=f"{what} loop-2 output")
+    g_lg = np32(step.logits1).reshape(R, -1)
+    got_lg = [g_lg[x, : lens[i] + 1] for i, x in enumerate(rows)]
+    rest = restated_dense_logits(layer, 1, rows, q[1], kc[1], SCALING)
+    assert_close(np.concatenate(got_lg), np.concatenate(rest), max_abs=1e-4, mean_abs=1e-5,
+                 what=f"{what} logits vs restated reader arithmetic")
+    assert_close(np.concatenate(got_lg), np.concatenate([np.asarray(x) for x in lg1]), max_abs=2e-2, mean_abs=5e-3,
+                 what=f"{what} logits vs oracle bf16 chain")
+    cap = step.indices.shape[-1]
+    idx = step.indices.cpu().numpy().reshape(R, cap)
+    sel = OA.decode_topk(got_lg, 0.10, kpad=cap)
+    assert np.array_equal(idx[rows], sel.indices), f"{what} selection"
+    so = OA.selected_value_aggregate(sel.indices, sel.valid, sel.selected_weights, Vr[1], vc[1], lens)
+    assert_close(np32(step.selected_output).reshape(R, 128)[rows], so, what=f"{what} selected output")
+    for loop, got in ((2, step.delta2), (3, step.delta3)):
+        want = OA.sparse_delta(q[loop], Kr[loop], Vr[loop], kc[loop], vc[loop], lens, sel.indices, sel.valid,
+                               so, sel.mass, SCALING)
+        assert_close(np32(got).reshape(R, 128)[rows], want, what=f"{what} loop-{loop + 1} delta")
+    return sel
+
+
+def _run_step(w, layer):
+    qs = [q.contiguous() for q in w.queries]
+    cur = [w.current(r) for r in range(4)]
+    step = decode_attention_step(layer, qs, [c[0] for c in cur], [c[1] for c in cur], SCALING, 0.10)
+    torch.cuda.synchronize()
+    for t in (step.out0, step.out1, step.delta2, step.delta3, step.selected_output):
+        assert bool(torch.isfinite(t).all())
+    return step
+
+
+@pytest.mark.parametrize("which", ["shortest", "longest"])
+def test_cfg2_ragged_batch32(which):
+    """cfg2 at its shape; every head of the shortest / the longest sequence."""
+    print(f"case: cfg2 B32 H16 ragged [1024, 16384], {which} sequence", flush=True)
     B, H = 32, 16
     lengths = ragged_lengths(B, 1024, 16384, seed=2)
-    w = decode_workload(B, H, 0, seed=2, lengths=lengths)
-    Tmax = max(lengths)
+    assert max(lengths) <= 16384 and min(lengths) >= 1024
+    w = decode_workload(B, H, 0, seed=2, lengths=lengths, device=DEV)
     layer = _layer([w.cache(r)[0] for r in range(4)], [w.cache(r)[1] for r in range(4)], lengths=lengths)
-    qs = [w.queries[r].to(DEV) for r in range(4)]
-    cur = [w.current(r) for r in range(4)]
-    step = decode_attention_step(layer, qs, [c[0].to(DEV) for c in cur], [c[1].to(DEV) for c in cur], SCALING, 0.10)
-    torch.cuda.synchronize()
-    R = B * H
-    out1 = np32(step.out1).reshape(R, 128)
-    d2 = np32(step.delta2).reshape(R, 128)
-    d3 = np32(step.delta3).reshape(R, 128)
-    g_lg = np32(step.logits1).reshape(R, -1)
-    cap = step.indices.shape[-1]
-    idx = step.indices.cpu().numpy().reshape(R, cap)
-    assert np.isfinite(out1).all() and np.isfinite(d2).all() and np.isfinite(d3).all()
-    heads = [0, H - 1]
-    for b in (int(np.argmin(lengths)), int(np.argmax(lengths))):
-        t = lengths[b]
-        ks = [w.keys[r][b:b + 1, heads, :t] for r in range(4)]
-        vs = [w.values[r][b:b + 1, heads, :t] for r in range(4)]
-        nk, nv, chain, tp = oracle_prefix(ks, vs)
-        Kb, Vb = materialized(nk, nv, chain, tp)
-        rows = [b * H + h for h in heads]
-        q = [np32(w.queries[r]).reshape(R, 128)[rows] for r in range(4)]
-        kc = [np32(c[0]).reshape(R, 128)[rows] for c in cur]
-        vc = [np32(c[1]).reshape(R, 128)[rows] for c in cur]
-        Kr = [flat_rows(Kb[r]) for r in range(4)]
-        Vr = [flat_rows(Vb[r]) for r in range(4)]
-        o1, _ = OA.dense_decode(q[1], Kr[1], Vr[1], kc[1], vc[1], SCALING)
-        assert_close(out1[rows], o1, what=f"cfg2 b={b} (T={t}) loop-2 output")
-        sel = OA.decode_topk([g_lg[r, : t + 1] for r in rows], 0.10, kpad=cap)
-        assert np.array_equal(idx[rows], sel.indices), f"cfg2 b={b} selection"
-        so = OA.selected_value_aggregate(sel.indices, sel.valid, sel.selected_weights, Vr[1], vc[1], [t, t])
-        for loop, got in ((2, d2), (3, d3)):
-            want = OA.sparse_delta(q[loop], Kr[loop], Vr[loop], kc[loop], vc[loop], [t, t], sel.indices, sel.valid,
-                                   so, sel.mass, SCALING)
-            assert_close(got[rows], want, what=f"cfg2 b={b} loop-{loop + 1} delta")
-    assert Tmax <= 16384
+    step = _run_step(w, layer)
+    b = int(np.argmin(lengths)) if which == "shortest" else int(np.argmax(lengths))
+    rows = [b * H + h for h in range(H)]
+    sel = _check_rows(w, layer, step, rows, H, lengths, f"cfg2 b={b} (T={lengths[b]})")
+    assert list(sel.count) == [OA.decode_budget(lengths[b] + 1, 0.10)] * H
 
 
-def test_cfg3_full_shape_rows():
+def cfg3_boundary_rows(B=8, H=16, T=32768, per_split=8):
+    """Rows of cfg3 where a dense reader's persistent-wave range begins: a row spans
+    3 tail units + Tp/64 prefix groups of the global work sequence, and the waves split
+    it into contiguous ranges of ceil(U / waves) units.  For both reader grids on a
+    256-CU part (1024 waves: loop 2, one workgroup per CU; 2048 waves: loop 1, two) the
+    rows whose first range boundary falls earliest after the row start -- at the tail, or
+    between the tail and the first prefix group -- are taken; every row also has
+    boundaries mid-prefix (a row spans 8-16 ranges)."""
+    span = 3 + (T - 64) // 64
+    U = B * H * span
+    out = []
+    for waves in (1024, 2048):
+        chunk = -(-U // waves)
+        off = [(-(r * span)) % chunk for r in range(B * H)]
+        for r in sorted(range(B * H), key=lambda r: (off[r], r)):
+            if r not in out:
+                out.append(r)
+            if len(out) % per_split == 0 and len(out) >= per_split * (1 + (waves == 2048)):
+                break
+    return out
+
+
+@pytest.mark.parametrize("half", [0, 1])
+def test_cfg3_full_shape_rows(half):
     """cfg3 at its full shape (B8 H16 T32768, the benchmark workload): one decode step over
-    every row on the GPU; two rows (first and last) are checked against the oracle."""
-    print("case: cfg3 B8 H16 T32768", flush=True)
+    every row on the GPU; 8 of the 16 wave-boundary rows per half are checked."""
     B, H, T = 8, 16, 32768
-    w = decode_workload(B, H, T, seed=3)
+    rows = cfg3_boundary_rows(B, H, T)[8 * half: 8 * half + 8]
+    print(f"case: cfg3 B8 H16 T32768 rows {rows}", flush=True)
+    w = decode_workload(B, H, T, seed=3, device=DEV)
     layer = _layer([w.cache(r)[0] for r in range(4)], [w.cache(r)[1] for r in range(4)])
-    qs = [w.queries[r].to(DEV) for r in range(4)]
-    cur = [w.current(r) for r in range(4)]
-    step = decode_attention_step(layer, qs, [c[0].to(DEV) for c in cur], [c[1].to(DEV) for c in cur], SCALING, 0.10)
-    torch.cuda.synchronize()
-    R = B * H
-    out0 = np32(step.out0).reshape(R, 128)
-    out1 = np32(step.out1).reshape(R, 128)
-    d2 = np32(step.delta2).reshape(R, 128)
-    d3 = np32(step.delta3).reshape(R, 128)
-    g_lg = np32(step.logits1).reshape(R, -1)
-    cap = step.indices.shape[-1]
-    idx = step.indices.cpu().numpy().reshape(R, cap)
-    for a in (out0, out1, d2, d3):
-        assert np.isfinite(a).all()
-    for b, h in ((0, 0), (B - 1, H - 1)):
-        ks = [w.keys[r][b:b + 1, h:h + 1, :T] for r in range(4)]
-        vs = [w.values[r][b:b + 1, h:h + 1, :T] for r in range(4)]
-        nk, nv, chain, tp = oracle_prefix(ks, vs)
-        Kb, Vb = materialized(nk, nv, chain, tp)
-        rows = [b * H + h]
-        q = [np32(w.queries[r]).reshape(R, 128)[rows] for r in range(4)]
-        kc = [np32(c[0]).reshape(R, 128)[rows] for c in cur]
-        vc = [np32(c[1]).reshape(R, 128)[rows] for c in cur]
-        Kr = [flat_rows(Kb[r]) for r in range(4)]
-        Vr = [flat_rows(Vb[r]) for r in range(4)]
-        o0, _ = OA.dense_decode(q[0], Kr[0], Vr[0], kc[0], vc[0], SCALING)
-        o1, _ = OA.dense_decode(q[1], Kr[1], Vr[1], kc[1], vc[1], SCALING)
-        assert_close(out0[rows], o0, what=f"cfg3 row {rows[0]} loop-1 output")
-        assert_close(out1[rows], o1, what=f"cfg3 row {rows[0]} loop-2 output")
-        sel = OA.decode_topk([g_lg[r, : T + 1] for r in rows], 0.10, kpad=cap)
-        assert np.array_equal(idx[rows], sel.indices), f"cfg3 row {rows[0]} selection"
-        assert sel.count[0] == 3277
-        so = OA.selected_value_aggregate(sel.indices, sel.valid, sel.selected_weights, Vr[1], vc[1], [T])
-        for loop, got in ((2, d2), (3, d3)):
-            want = OA.sparse_delta(q[loop], Kr[loop], Vr[loop], kc[loop], vc[loop], [T], sel.indices, sel.valid,
-                                   so, sel.mass, SCALING)
-            assert_close(got[rows], want, what=f"cfg3 row {rows[0]} loop-{loop + 1} delta")
+    step = _run_step(w, layer)
+    sel = _check_rows(w, layer, step, rows, H, [T] * B, "cfg3")
+    assert list(sel.count) == [3277] * len(rows)

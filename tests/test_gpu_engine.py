@@ -1,5 +1,7 @@
 """End-to-end FlashLoopEngine on the HIP kernels (tiny random-init Ouro-shaped model)."""
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -156,3 +158,97 @@ def test_saved_cache_decodes_identically(tmp_path):
         da = a.decode(ids[:, i:i + 1])
         db = b.decode(ids[:, i:i + 1])
         assert torch.equal(da.logits, db.logits), f"step {i}"
+
+
+def test_sparse_decode_disabled_runs_every_loop_dense():
+    """enable_sparse_decode=False (flashloop/engine.py:422): loops 3-4 read the cache
+    densely like loops 1-2; the step tracks the dense model, graphs equal eager."""
+    model = OuroForCausalLM.random_init(TINY, seed=9, device="cuda")
+    cfg = FlashLoopConfig(prefill_fraction_loop3=1.0, prefill_fraction_loop4=1.0, enable_sparse_decode=False)
+    eager = FlashLoopEngine(model, config=cfg, use_graphs=False)
+    graphed = FlashLoopEngine(model, config=cfg, use_graphs=True)
+    ids = _ids(200, seed=9)
+    eager.prefill(ids[:, :190], decode_capacity=32)
+    graphed.prefill(ids[:, :190], decode_capacity=32)
+    for i in range(190, 200):
+        da = eager.decode(ids[:, i:i + 1])
+        db = graphed.decode(ids[:, i:i + 1])
+        assert torch.equal(da.logits, db.logits), f"step {i}"
+        ref = model.dense_forward(ids[:, :i + 1])
+        assert _cos(da.logits, ref) > 0.98
+    nl = TINY.num_hidden_layers
+    assert da.receipt.dense_attention_calls == 4 * nl and da.receipt.sparse_attention_calls == 0
+    assert da.receipt.dense_late_loop_calls == 2 * nl and da.receipt.selected_keys_per_layer == ()
+
+
+def test_graph_recapture_releases_old_graphs():
+    """Each recapture destroys the superseded graph and its pool before capturing (no
+    garbage-collector workaround): many recaptures with collections in between."""
+    import gc
+
+    model = OuroForCausalLM.random_init(TINY, seed=10, device="cuda")
+    eng = FlashLoopEngine(model, config=FlashLoopConfig(decode_key_fraction=1.0), use_graphs=True)
+    ids = _ids(400, seed=10)
+    eng.prefill(ids[:, :200], decode_capacity=256)
+    held = []
+    graphs = set()
+    for i in range(200, 330):  # fraction 1: the selection capacity steps every 64 keys
+        out = eng.decode(ids[:, i:i + 1])
+        held.append(out)  # outputs held across recaptures stay valid tensors
+        graphs.add(id(eng._runner.graph))
+        gc.collect()
+    assert len(graphs) >= 3
+    assert all(torch.isfinite(o.logits).all() for o in held[-3:])
+
+
+def test_cfg4_full_model_prefill_and_decode():
+    """BASELINE config 4 at its shape: the random-init 24-layer looped decoder (hidden
+    2048, 16 heads x 128, SwiGLU 5632, vocab 49152), an 8192-token prompt, then 70 greedy
+    decode steps (one rollover of the BF16 tail).  Checks the prefill receipts, the
+    loop-2 key budget ceil((T+1)*0.1) actually selected by the top-k kernel at every step,
+    finite logits, graph replay equal to eager launches bit for bit, and each step's
+    logits against the torch-module decode step (fused_decode=False) by cosine."""
+    print("case: cfg4 24L/2048/5632/49152, prompt 8192, 70 steps", flush=True)
+    cfg = OuroConfig()
+    assert (cfg.num_hidden_layers, cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size) == (24, 2048, 5632, 49152)
+    model = OuroForCausalLM.random_init(cfg, seed=4, device="cuda")
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, cfg.vocab_size, (1, 8192), generator=g).cuda()
+    graphed = FlashLoopEngine(model, use_graphs=True)
+    eager = FlashLoopEngine(model, use_graphs=False)
+    modules = FlashLoopEngine(model, use_graphs=False)
+    modules.fused_decode = False
+    outs = [e.prefill(ids, decode_capacity=128) for e in (graphed, eager, modules)]
+    for o in outs:
+        assert [(r.loop, r.total_rows, r.active_rows) for r in o.state.prefill_receipts] == \
+            [(1, 8192, 8192), (2, 8192, 8192), (3, 8192, 2048), (4, 8192, 820)]
+        assert torch.isfinite(o.logits).all()
+    assert torch.equal(outs[0].logits, outs[1].logits)
+    lc = eager.state.cache.layers[0]
+    assert lc.quantized_tokens == 8128
+    seen = []
+    orig = lc.select_decode_keys
+
+    def spy(logits, fraction, validate=False):
+        res = orig(logits, fraction, validate=True)  # NaN/inf logits would raise here
+        seen.append(res[4])
+        return res
+
+    lc.select_decode_keys = spy
+    tok = torch.argmax(outs[0].logits, dim=-1, keepdim=True)
+    worst = 1.0
+    for step in range(70):
+        pos = 8192 + step
+        a = graphed.decode(tok)
+        b = eager.decode(tok)
+        c = modules.decode(tok)
+        assert torch.isfinite(a.logits).all()
+        assert torch.equal(a.logits, b.logits), f"step {step}: graph replay differs from eager"
+        worst = min(worst, _cos(b.logits, c.logits))
+        assert _cos(b.logits, c.logits) > 0.999, f"step {step}: fused vs torch-module step"
+        want_k = math.ceil((pos + 1) * 0.1)  # T = pos keys before the current token
+        assert a.receipt.selected_keys_per_layer == (want_k,) * 24
+        assert seen[-1].cpu().tolist() == [want_k] * 16, f"step {step}: observed top-k budget"
+        tok = torch.argmax(a.logits, dim=-1, keepdim=True)
+    print(f"[parity] cfg4 worst cosine fused vs modules {worst:.6f}", flush=True)
+    assert lc.quantized_tokens == 8192  # one 64-token group rolled out of the tail
