@@ -65,6 +65,8 @@ SIGNATURES = {
     "fl_pack_kv_groups": (_I32, [_VIEW, _I32, _PP, _PP, _I64, _I32, _PP, _I64, _P, _I32, _PP, _PP, _P]),
     "fl_decode_attn_dense_workspace": (_SZ, [_VIEW]),
     "fl_decode_attn_dense": (_I32, [_VIEW, _I32, _P, _P, _P, _F32, _P, _P, _I64, _P, _SZ, _P]),
+    "fl_decode_attn_dense_noalloc_max_bytes": (_SZ, []),
+    "fl_decode_attn_dense_noalloc": (_I32, [_VIEW, _I32, _P, _P, _P, _F32, _P, _P, _I64, _P]),
     "fl_decode_attn_dense_pair_workspace": (_SZ, [_VIEW]),
     "fl_decode_attn_dense_pair": (_I32, [_VIEW, _P, _P, _P, _P, _P, _P, _P, _P, _F32, _P, _I64, _P, _SZ, _P]),
     "fl_profile_dense_reader": (_I32, [_I32, _I32]),

@@ -942,16 +942,12 @@ int32_t dense_checks(const fl_cache_view* view, int32_t loop, const uint16_t* q,
 }  // namespace
 }  // namespace fl
 
-extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop, const uint16_t* q,
-                                        const uint16_t* k_cur, const uint16_t* v_cur, float scaling, float* out,
-                                        float* logits, int64_t logits_stride, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
-  using namespace fl;
-  clear_error();
-  if (const int32_t rc = dense_checks(view, loop, q, k_cur, v_cur, out, logits, logits_stride, workspace); rc != FL_OK)
-    return rc;
-  const fl_cache_view& v = *view;
-  FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense: workspace too small");
+namespace fl {
+namespace {
+// One dense read on a checked workspace: the reader launch and its merge.
+int32_t dense_launch(const fl_cache_view& v, int32_t loop, const uint16_t* q, const uint16_t* k_cur,
+                     const uint16_t* v_cur, float scaling, float* out, float* logits, int64_t logits_stride,
+                     float* ws, hipStream_t st) {
   DenseArgs a{};
   a.v = v;
   a.q = q;
@@ -960,14 +956,13 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   a.scaling = scaling;
   a.logits = logits;
   a.logits_stride = logits_stride;
-  a.ws = static_cast<float*>(workspace);
+  a.ws = ws;
   a.tail_k = v.tail_key[loop];
   a.tail_v = v.tail_value[loop];
   const int blocks = persist_blocks(v, occupancy_of(loop, logits != nullptr));
   a.waves = blocks * kWaves;
   // a row has at most waves + 1 prefix partials (see partial_slot) plus its tail partial
   FL_REQUIRE(a.waves + 2 <= kMergeMaxParts, "fl_decode_attn_dense: too many persistent waves for one merge");
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid(blocks), block(kThreads);
   profile_before(st, loop);
   const bool lg = logits != nullptr;
@@ -987,6 +982,75 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
                      static_cast<const float*>(a.ws), static_cast<const float*>(a.ws), a.waves, v, out, out, 1);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(merge)");
   return FL_OK;
+}
+
+// ---- the allocation-free entry point's scratch: partials of fl_decode_attn_dense_noalloc.
+// One copy per GPU, held until the process ends.  Host code never uses the array's name
+// as an address (on the host it is a stand-in symbol): each device's address comes from
+// hipGetSymbolAddress, called once per device with that device current.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+int32_t scratch_ptr(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("fl_decode_attn_dense_noalloc: no current HIP device");
+    return FL_E_LAUNCH;
+  }
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error(std::string("fl_decode_attn_dense_noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      return FL_E_LAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FL_OK;
+}
+}  // namespace
+}  // namespace fl
+
+extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop, const uint16_t* q,
+                                        const uint16_t* k_cur, const uint16_t* v_cur, float scaling, float* out,
+                                        float* logits, int64_t logits_stride, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  using namespace fl;
+  clear_error();
+  if (const int32_t rc = dense_checks(view, loop, q, k_cur, v_cur, out, logits, logits_stride, workspace); rc != FL_OK)
+    return rc;
+  FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense: workspace too small");
+  return dense_launch(*view, loop, q, k_cur, v_cur, scaling, out, logits, logits_stride, static_cast<float*>(workspace),
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t fl_decode_attn_dense_noalloc_max_bytes(void) { return fl::kScratchBytes; }
+
+extern "C" int32_t fl_decode_attn_dense_noalloc(const fl_cache_view* view, int32_t loop, const uint16_t* q,
+                                                const uint16_t* k_cur, const uint16_t* v_cur, float scaling,
+                                                float* out, float* logits, int64_t logits_stride, void* stream) {
+  using namespace fl;
+  clear_error();
+  FL_REQUIRE(view != nullptr, "fl_decode_attn_dense_noalloc: view is null");
+  const size_t need = fl_decode_attn_dense_workspace(view);
+  if (need > kScratchBytes) {
+    set_error("fl_decode_attn_dense_noalloc: the cache needs " + std::to_string(need) +
+              " bytes of partials, more than the static scratch holds (" + std::to_string(kScratchBytes) +
+              " bytes, about 7000 (batch, head) rows); use fl_decode_attn_dense with a workspace");
+    return FL_E_CAPACITY;
+  }
+  void* ws = nullptr;
+  if (const int32_t rc = scratch_ptr(&ws); rc != FL_OK) return rc;
+  if (const int32_t rc = dense_checks(view, loop, q, k_cur, v_cur, out, logits, logits_stride, ws); rc != FL_OK)
+    return rc;
+  return dense_launch(*view, loop, q, k_cur, v_cur, scaling, out, logits, logits_stride, static_cast<float*>(ws),
+                      static_cast<hipStream_t>(stream));
 }
 
 namespace {

@@ -152,6 +152,24 @@ int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
                              float scaling, float* out, float* logits, int64_t logits_stride,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Allocation-free form of fl_decode_attn_dense.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory or pass a workspace (code under HIP
+ * graph capture that must not call hipMalloc, tight serving loops, harnesses that
+ * forbid allocation).  Same arguments and results as fl_decode_attn_dense (bit for bit:
+ * the same kernels and grid), without the workspace: the per-split partials go to a
+ * static device array of fl_decode_attn_dense_noalloc_max_bytes() bytes (8 MiB), one
+ * per GPU, held until the process ends.  A cache whose partials exceed it (about 7000
+ * (batch, head) rows on a 256-CU GPU) is rejected with FL_E_CAPACITY.  It allocates
+ * nothing.  Every call on one GPU shares that GPU's array: calls that may overlap on
+ * one GPU (two streams, or two threads) race and must be ordered by the caller.
+ */
+size_t fl_decode_attn_dense_noalloc_max_bytes(void);
+int32_t fl_decode_attn_dense_noalloc(const fl_cache_view* view, int32_t loop,
+                                     const uint16_t* q, const uint16_t* k_cur, const uint16_t* v_cur,
+                                     float scaling, float* out, float* logits, int64_t logits_stride,
+                                     void* stream);
+
 /* Loops 1 and 2 of a decode step (streams 0 and 1; loop 2 with logits) in one reader
  * launch plus one merge launch.  Same results as fl_decode_attn_dense(loop 0) followed by
  * fl_decode_attn_dense(loop 1, logits): logits bit-identical, outputs within float
