@@ -11,10 +11,14 @@ selected aggregate from the rows it reads) and sparse loop 4
 ``value`` is the step's algorithmic HBM bytes / step time (GB/s); ``roofline`` reports
 the dense loop-2 reader kernel (the dominant kernel) against the 8 TB/s HBM peak, timed
 inside the timed steps with HIP events that the library records on the launch stream
-immediately around that kernel (fl_profile_dense_reader); ``cpu_baseline`` times the
-numpy oracle (a single-core restatement of the reference algorithm) on a bounded
-sample of (b,h) rows of the same workload (its step repeated for about --cpu-seconds) and
-scales it to a full step.
+immediately around that kernel (fl_profile_dense_reader); ``breakdown`` times each op of
+the step (reader + merge, HIP events on the launch stream) over extra steps after the
+timed region, with its algorithmic bytes and fraction of peak; ``cpu_baseline`` times
+the reference's torch path of the same step (oracle/torch_cpu.py: flashloop_torch's
+bf16 attention over the materialised loop caches, top-k mask, mass-scaled sparse
+outputs) on torch-CPU with every thread torch is given, on a bounded sample of (b,h)
+rows of the same workload (its step repeated for about --cpu-seconds), scaled to the
+full step.
 """
 
 from __future__ import annotations
@@ -48,7 +52,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-rows", type=int, default=16, help="(b,h) rows of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-rows", type=int, default=32, help="(b,h) rows of the CPU baseline sample (0 = skip)")
+    ap.add_argument("--breakdown-steps", type=int, default=10,
+                    help="extra steps after the timed region that time each op with HIP events (0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline: repeat the sample's step until this much CPU time has run")
     ap.add_argument("--eager", action="store_true", help="cfg4: eager decode launches instead of HIP-graph replay")
@@ -64,40 +70,52 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(cfg, rows: int, fraction: float, seconds: float):
-    """Time the numpy oracle's decode step on ``rows`` (b,h) rows of the workload, one core,
-    repeated until ``seconds`` of CPU time have run; returns (us per full step, seconds
-    timed, repetitions)."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def cpu_baseline(sample, fraction: float, seconds: float):
+    """Time the reference's torch path of the decode step (oracle/torch_cpu.py) on the
+    sampled rows, on torch-CPU with torch's thread count, repeated until ``seconds`` of
+    wall time have run.  ``sample``: (q, k_cur, v_cur, keys, values) CPU bf16 tensors.
+    Returns (seconds per step of the sample, seconds timed, repetitions, threads)."""
+    import torch
 
-    from flashloop_amd.synthetic import SCALING, decode_workload
-    from oracle import attention as OA
-    from oracle import codec
+    from flashloop_amd.synthetic import SCALING
+    from oracle import torch_cpu
 
-    w = decode_workload(1, rows, cfg["tokens"], seed=cfg["seed"] + 100)
-    nk = [w.cache(r)[0].float().numpy() for r in range(4)]
-    nv = [w.cache(r)[1].float().numpy() for r in range(4)]
-    chain, tp = codec.compress_prefix(nk, nv)
-    K, V = codec.materialize_loop_cache(nk, nv, chain, tp)
-    cur = [w.current(r) for r in range(4)]
-    q = [w.queries[r].float().numpy().reshape(rows, 128) for r in range(4)]
-    kc = [c[0].float().numpy().reshape(rows, 128) for c in cur]
-    vc = [c[1].float().numpy().reshape(rows, 128) for c in cur]
+    q, kc, vc, keys, values = sample
+    torch_cpu.decode_layer_step(q, kc, vc, keys, values, SCALING, fraction)  # warm-up (allocator, threads)
     reps = 0
-    with threadpool_limits(1):
-        t0 = time.perf_counter()
-        while True:
-            OA.decode_layer_step(q, kc, vc, [K[r][0] for r in range(4)], [V[r][0] for r in range(4)], SCALING,
-                                 fraction)
-            reps += 1
-            dt = time.perf_counter() - t0
-            if dt >= seconds or reps >= 256:
-                break
-    total_rows = cfg["batch"] * cfg["heads"]
-    us_step = dt / reps / rows * total_rows * 1e6
-    del np
-    return us_step, dt, reps
+    t0 = time.perf_counter()
+    while True:
+        torch_cpu.decode_layer_step(q, kc, vc, keys, values, SCALING, fraction)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds or reps >= 256:
+            break
+    return dt / reps, dt, reps, torch.get_num_threads()
+
+
+def cpu_sample(ks, vs, queries, kcur, vcur, rows: int, B: int, H: int, T: int):
+    """The first ``rows`` (b,h) rows of the workload as the reference's torch path holds
+    them: per loop the materialised bf16 cache (the codec's reconstruction of the packed
+    prefix -- built on the GPU, bit-identical to the oracle's -- then the BF16 tail)."""
+    import torch
+
+    from flashloop_amd import CrossLoopKVLayer
+
+    sub_k = [k.reshape(1, B * H, T, 128)[:, :rows].contiguous() for k in ks]
+    sub_v = [v.reshape(1, B * H, T, 128)[:, :rows].contiguous() for v in vs]
+    small = CrossLoopKVLayer.from_prefill(sub_k, sub_v, recon=True)
+    tp = small.quantized_tokens
+    keys, values = [], []
+    for r in range(4):
+        rk = small.recon_keys[r].reshape(rows, -1, 128)[:, :tp]
+        rv = small.recon_values[r].reshape(rows, -1, 128)[:, :tp]
+        keys.append(torch.cat([rk, sub_k[r][0, :, tp:T]], dim=1).cpu())
+        values.append(torch.cat([rv, sub_v[r][0, :, tp:T]], dim=1).cpu())
+    flat = lambda t: t.reshape(B * H, 1, 128)[:rows].cpu()  # noqa: E731
+    out = ([flat(x) for x in queries], [flat(x) for x in kcur], [flat(x) for x in vcur], keys, values)
+    del small
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_cfg4(args):
@@ -190,10 +208,13 @@ def main():
     torch.cuda.synchronize()
     pack_s = time.perf_counter() - t0
     pack_bytes = 8 * B * H * T * 128 * 2  # bf16 inputs of 4 loops K and V (read once)
-    del ks, vs
-    torch.cuda.empty_cache()
     kcur = [c[0] for c in cur]
     vcur = [c[1] for c in cur]
+    sample = None
+    if args.cpu_rows > 0:
+        sample = cpu_sample(ks, vs, queries, kcur, vcur, min(args.cpu_rows, B * H), B, H, T)
+    del ks, vs
+    torch.cuda.empty_cache()
     if args.calib_copy_mib > 0:
         src = torch.ones(args.calib_copy_mib * 2**18, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
@@ -212,22 +233,37 @@ def main():
 
     lib = _lib.load()
 
-    def timed_step(i):
+    def timed_step(i, ev=None):
+        """One step; with ``ev`` (a list) a HIP event is recorded on the launch stream
+        before the first op and after each op (the per-op breakdown)."""
+
+        def mark():
+            if ev is not None:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record()
+                ev.append(e)
+
+        mark()
         if (not args.paired_dense):
             out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=kcur[0], current_value=vcur[0],
                                                    scaling=SCALING, return_logits=False)
+            mark()
             out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=kcur[1],
                                                         current_value=vcur[1], scaling=SCALING, return_logits=True)
         else:
             out0, out1, logits = layer.dense_source_attention_pair(
                 queries=queries[:2], current_keys=kcur[:2], current_values=vcur[:2], scaling=SCALING)
+        mark()
         idx, valid, mass, wts, counts = layer.select_decode_keys(logits, args.fraction)
+        mark()
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
             source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)
+        mark()
         d3 = layer.cached_mass_sparse_attention_delta(3, query=queries[3], current_key=kcur[3], current_value=vcur[3],
                                                       indices=idx, valid=valid, source_selected_output=so,
                                                       global_mass=mass, scaling=SCALING)
+        mark()
         return out0, out1, d2, d3
 
     for _ in range(args.warmup):
@@ -270,19 +306,43 @@ def main():
     reader_gbps = reader_bytes / (reader_ms * 1e-3) / 1e9
     finite = all(bool(torch.isfinite(t).all()) for t in (ref.out0, ref.out1, ref.delta2, ref.delta3))
 
+    # per-op breakdown: extra steps after the timed region, events between the ops
+    breakdown = None
+    if args.breakdown_steps > 0:
+        names = (["dense_loop1", "dense_loop2"] if not args.paired_dense else ["dense_loop1+2"]) + \
+            ["topk", "sparse_loop3_with_source", "sparse_loop4"]
+        evs = []
+        for i in range(args.breakdown_steps):
+            ev = []
+            timed_step(i, ev)
+            evs.append(ev)
+        torch.cuda.synchronize()
+        breakdown = {}
+        for j, name in enumerate(names):
+            us = sum(ev[j].elapsed_time(ev[j + 1]) for ev in evs) / len(evs) * 1e3
+            nbytes = parts[name] if name in parts else parts["dense_loop1"] + parts["dense_loop2"]
+            ach = nbytes / (us * 1e-6) / 1e9
+            breakdown[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes, "GB_per_s": round(ach, 1),
+                               "frac": round(ach / HBM_PEAK_GBPS, 4)}
+        breakdown["note"] = ("HIP events between the ops of extra steps: an op's time holds its reader, its merge "
+                             "and the launch gaps the events add; per-kernel times are in the rocprof summary")
+
     cpu = None
-    if args.cpu_rows > 0:
-        print(f"[bench] CPU baseline on {args.cpu_rows} rows", file=sys.stderr, flush=True)
-        us_cpu, dt, reps = cpu_baseline(cfg, args.cpu_rows, args.fraction, args.cpu_seconds)
+    if sample is not None:
+        rows = sample[0][0].shape[0]
+        print(f"[bench] CPU baseline on {rows} rows", file=sys.stderr, flush=True)
+        s_step, dt, reps, threads = cpu_baseline(sample, args.fraction, args.cpu_seconds)
+        us_cpu = s_step * (B * H) / rows * 1e6
         cpu = {
             "value": round(step_bytes / (us_cpu * 1e-6) / 1e9, 4),
             "unit": "GB/s",
             "us_per_step": round(us_cpu, 1),
-            "cores": 1,
+            "cores": threads,
             "kind": "port",
-            "sample": f"{args.cpu_rows} of {B * H} (b,h) rows of the same workload, the decode step "
-                      f"repeated {reps} times ({dt:.1f} s on one core, numpy oracle), scaled by "
-                      f"{B * H}/{args.cpu_rows}",
+            "sample": f"{rows} of {B * H} (b,h) rows of the same workload at full context: flashloop_torch's "
+                      f"decode step (oracle/torch_cpu.py: bf16 attention over the materialised caches of all "
+                      f"4 loops, top-k mask, mass-scaled sparse outputs) on torch-CPU with {threads} threads, "
+                      f"repeated {reps} times ({dt:.1f} s), scaled by {B * H}/{rows}",
         }
 
     line = {
@@ -298,11 +358,11 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "int4 codes x fp16 scale/min, f32 accumulate",
         "data": "synthetic",
         "config": {
             "workload": f"{args.config}: decode attention of one layer, 4 loops, B={B} H={H} D=128 T={T}, "
-                        f"int4 residual streams g64 (f32 scale/min), BF16 tail {tail[0]}, "
+                        f"int4 residual streams g64 (fp32 scale/min stored, fp16 copies streamed), BF16 tail {tail[0]}, "
                         f"late loops on top {args.fraction:.0%} keys",
             "batch": B,
             "heads": H,
@@ -323,6 +383,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "breakdown_bytes": parts,
+        "breakdown": breakdown,
         "pack": {"GB_read_per_s": round(pack_bytes / pack_s / 1e9, 1), "seconds": round(pack_s, 4),
                  "note": "one-off cache build (J1) incl. host setup, not part of the step"},
         "finite": finite,
