@@ -595,3 +595,36 @@ def test_topk_reports_non_finite_scores(n):
     with pytest.raises(ValueError):
         kernels.decode_topk(t, nk, 0.1, cap, validate=True)
     kernels.decode_topk(t[:1], nk[:1], 0.1, cap, validate=True)  # finite row passes
+
+
+def test_topk_crowded_boundary_bin_and_very_long_rows():
+    """Scores clustered in one 12-bit key prefix (more boundary candidates than the split
+    kernel's LDS list holds: the exact ranking reads the row instead), with exact ties at
+    the boundary; and rows past the split kernels' 65536 keys (one-workgroup kernel)."""
+    print("case: topk crowded bin / 70000-key rows", flush=True)
+    rng = np.random.default_rng(12)
+    n = 40000
+    lg = np.empty((3, n), np.float32)
+    lg[0] = 1.0 + rng.random(n).astype(np.float32) * 0.1  # one prefix bin [1, 1.125)
+    lg[1] = 1.0 + np.round(rng.random(n) * 64).astype(np.float32) / 1024  # one bin, heavy ties
+    lg[2] = np.float32(1.0)  # all equal
+    for frac in (0.1, 0.5):
+        cap = OA.padded_capacity(OA.decode_budget(n, frac))
+        idx, valid, mass, wts, counts = kernels.decode_topk(torch.from_numpy(lg).to(DEV),
+                                                            torch.full((3,), n, dtype=torch.int32, device=DEV),
+                                                            frac, cap)
+        torch.cuda.synchronize()
+        sel = OA.decode_topk(lg, frac, kpad=cap)
+        assert np.array_equal(idx.cpu().numpy(), sel.indices), f"crowded indices differ at {frac}"
+        assert np.allclose(mass.cpu().numpy(), sel.mass, rtol=2e-6)
+        assert np.allclose(wts.cpu().numpy(), sel.selected_weights, rtol=2e-5, atol=1e-8)
+    n = 70000
+    lg = (rng.standard_normal((2, n)) * 2.0).astype(np.float32)
+    lg[1] = np.round(lg[1] * 4.0) / 4.0
+    cap = OA.padded_capacity(OA.decode_budget(n, 0.1))
+    idx, valid, mass, wts, counts = kernels.decode_topk(torch.from_numpy(lg).to(DEV),
+                                                        torch.full((2,), n, dtype=torch.int32, device=DEV), 0.1, cap)
+    torch.cuda.synchronize()
+    sel = OA.decode_topk(lg, 0.1, kpad=cap)
+    assert np.array_equal(idx.cpu().numpy(), sel.indices)
+    assert np.allclose(mass.cpu().numpy(), sel.mass, rtol=2e-6)
