@@ -86,3 +86,77 @@ def sparse_bytes(stats, cap: int, loop: int, with_source: bool = False) -> int:
         tot += s["other"] * 2 * BF16_ROW
         tot += 3 * BF16_ROW + 128 * 4 + 4 + 128 * 4 + cap * 5
     return tot
+
+
+# ---------------------------------------------------------------------------------
+# The reference's own accounting, for the audit fields a drop-in must report with the
+# reference's values: the codec's byte count of a temporal group
+# (flashloop_torch/kv_quantization.py:489-527, 606-620), the streaming compressor's
+# audit (kv_quantization.py:246-322) and the storage of a reference cache layer in its
+# KIVI layout (flashloop/cache.py:1084-1101; tensor shapes kivi_backend.py:346-360).
+# ---------------------------------------------------------------------------------
+def codec_group_bytes(batch: int, heads: int, channels: int, group_tokens: int, transition_active,
+                      bits: int = 4, group_size: int = 64) -> int:
+    """Packed bytes of one temporal group of the residual chain: the anchor and every
+    transition's active rows, K per channel (one 4-byte fp16 (scale, min) pair per
+    channel of each stream holding a row) and V per token (one pair per 64 channels of
+    each active token)."""
+    pairs_v = -(-channels // group_size)
+    total = 0
+    for tokens in [batch * group_tokens, *[int(x) for x in transition_active]]:
+        if tokens == 0:
+            continue
+        payload = -(-tokens * heads * channels * bits // 8)
+        total += 2 * payload + 4 * (batch * heads * channels) + 4 * (tokens * heads * pairs_v)
+    return total
+
+
+def codec_audit(*, num_layers: int, batch: int, heads: int, channels: int, total_tokens: int,
+                current_tokens: int, quantized_tokens: int, group_bytes, mask_numel: int | None,
+                recurrent_steps: int = 4) -> dict:
+    """The compressor audit's byte fields from the per-(layer, group) packed bytes."""
+    packed = int(sum(group_bytes))
+    tail = total_tokens - quantized_tokens
+    per_token = num_layers * recurrent_steps * 2 * batch * heads * channels * 2
+    residual = per_token * tail
+    dense = per_token * total_tokens
+    masks = -(-2 * int(mask_numel) // 8) if mask_numel is not None else 0
+    total = packed + residual + masks
+    return {
+        "quantized_groups": len(group_bytes),
+        "quantized_tokens": quantized_tokens,
+        "bf16_tail_tokens": tail,
+        "total_cache_tokens": total_tokens,
+        "current_cache_tokens": current_tokens,
+        "packed_stream_bytes": packed,
+        "residual_bf16_bytes": residual,
+        "mask_bytes": masks,
+        "total_packed_bytes": total,
+        "dense_recurrent_bf16_bytes": dense,
+        "dense_r4_bf16_bytes": dense if recurrent_steps == 4 else None,
+        "dense_recurrent_ratio": total / dense if dense else None,
+        "dense_r4_ratio": total / dense if recurrent_steps == 4 and dense else None,
+    }
+
+
+def reference_layer_storage_bytes(*, batch: int, heads: int, channels: int, packed_tokens: int, tail_tokens: int,
+                                  rows_loop3: int, rows_loop4: int, group_size: int = 64) -> int:
+    """What ``CrossLoopKVLayer.storage_bytes`` of the reference reports for the same
+    cache built by prefill with the KIVI reader: per packed stream (anchor and loop-2
+    residual over the prefix, loop-3/4 residuals over their compact rows) an int32
+    payload of 8 codes per word (K token-packed, V channel-packed) and fp16 minimum and
+    scale (K per channel per 64 rows, V per token per 64 channels); the four loops' BF16
+    tails; int64 override positions, int32 rank maps over the prefix and the two bool
+    tail-activity rows."""
+    total = 0
+    for rows in (packed_tokens, packed_tokens, rows_loop3, rows_loop4):
+        if rows == 0:
+            continue
+        k_payload = 4 * batch * heads * (-(-rows // 8)) * channels
+        k_meta = 2 * 2 * batch * heads * (-(-rows // group_size)) * channels
+        v_payload = 4 * batch * heads * (-(-channels // 8)) * rows
+        v_meta = 2 * 2 * batch * heads * rows * (-(-channels // group_size))
+        total += k_payload + k_meta + v_payload + v_meta
+    total += 4 * 2 * 2 * batch * heads * tail_tokens * channels
+    total += 8 * (rows_loop3 + rows_loop4) + 4 * 2 * packed_tokens + 2 * batch * tail_tokens
+    return total

@@ -93,7 +93,7 @@ class _PrefillLoops:
     mask3: torch.Tensor  # [1, T] bool
     mask4: torch.Tensor
     receipts: tuple
-    logits: torch.Tensor  # [1, vocab] f32
+    logits: torch.Tensor  # [1, vocab] f32 (or [1, T, vocab] with all_logits)
 
 
 class DecodeRunner:
@@ -290,7 +290,8 @@ class FlashLoopEngine:
         n = int(counts[0].item())  # prefill syncs once per loop boundary, as the reference does
         return mask, positions[0, :n].contiguous(), score
 
-    def _prefill_loops(self, input_ids: torch.Tensor, stage: Callable[[str], None] = lambda _n: None) -> "_PrefillLoops":
+    def _prefill_loops(self, input_ids: torch.Tensor, stage: Callable[[str], None] = lambda _n: None,
+                       all_logits: bool = False) -> "_PrefillLoops":
         """The four prefill loops of one sequence ``[1, T]`` (flashloop/engine.py:176-333):
         dense loops 1-2, then token-sparse loops 3-4 on the rows selected by the hidden
         delta score.  Returns every layer's K/V of every loop, the masks and the logits."""
@@ -312,14 +313,15 @@ class FlashLoopEngine:
         stage("loop4_sparse")
         receipts = (PrefillReceipt(1, t, t), PrefillReceipt(2, t, t), PrefillReceipt(3, t, pos3.numel()),
                     PrefillReceipt(4, t, pos4.numel()))
-        return _PrefillLoops([k1, k2, k3, k4], [v1, v2, v3, v4], mask3, mask4, receipts,
-                             self.model.lm_head(h4[:, -1]).float())
+        logits = self.model.lm_head(h4 if all_logits else h4[:, -1]).float()
+        return _PrefillLoops([k1, k2, k3, k4], [v1, v2, v3, v4], mask3, mask4, receipts, logits)
 
     @torch.inference_mode()
     def prefill(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None, *,
                 decode_capacity: int | None = None,
-                stage_observer: Callable[[str], None] | None = None) -> PrefillOutput:
-        """``FlashLoopEngine.prefill`` (flashloop/engine.py:161-344)."""
+                stage_observer: Callable[[str], None] | None = None, all_logits: bool = False) -> PrefillOutput:
+        """``FlashLoopEngine.prefill`` (flashloop/engine.py:161-344).  ``all_logits`` returns
+        the logits of every prompt position ``[1, T, vocab]`` instead of the last one."""
 
         def stage(name: str) -> None:
             if stage_observer is not None:
@@ -335,7 +337,7 @@ class FlashLoopEngine:
             raise ValueError("prefill requires at least one prompt token")
         if attention_mask is not None and (attention_mask.shape != input_ids.shape or not bool(attention_mask.bool().all())):
             raise ValueError("padding is not supported by the batch-one engine")
-        loops = self._prefill_loops(input_ids, stage)
+        loops = self._prefill_loops(input_ids, stage, all_logits=all_logits)
         cap = t + (self.config.decode_capacity if decode_capacity is None else int(decode_capacity))
         cache = CrossLoopKVCache(num_layers=len(self.layers))
         for li in range(len(self.layers)):

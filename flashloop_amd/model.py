@@ -38,6 +38,42 @@ class OuroConfig:
     eos_token_id: int | None = None
     init_std: float = 0.02
 
+    @classmethod
+    def from_hf_config(cls, raw: dict) -> "OuroConfig":
+        """The fields this model uses from a Hugging Face Ouro ``config.json``; every other
+        key is ignored.  ``head_dim`` defaults to hidden/heads.  Variants the engine does not
+        implement are refused here (flashloop/config.py:92-134): another ``model_type``,
+        sliding-window attention, non-full attention layers."""
+        mt = raw.get("model_type")
+        if mt is not None and mt != "ouro":
+            raise ValueError(f"config.json: model_type {mt!r} is not an Ouro checkpoint")
+        if raw.get("sliding_window") is not None and raw.get("use_sliding_window", True):
+            raise ValueError("config.json: sliding-window attention is not supported")
+        lt = raw.get("layer_types")
+        if lt is not None and set(lt) != {"full_attention"}:
+            raise ValueError("config.json: every layer must use full attention")
+        hidden = int(raw["hidden_size"])
+        heads = int(raw["num_attention_heads"])
+        kw = dict(
+            vocab_size=int(raw["vocab_size"]),
+            hidden_size=hidden,
+            intermediate_size=int(raw["intermediate_size"]),
+            num_hidden_layers=int(raw["num_hidden_layers"]),
+            num_attention_heads=heads,
+            num_key_value_heads=int(raw.get("num_key_value_heads", heads)),
+            head_dim=int(raw.get("head_dim") or hidden // heads),
+            rms_norm_eps=float(raw.get("rms_norm_eps", 1e-6)),
+            rope_theta=float(raw.get("rope_theta", 10000.0)),
+            total_ut_steps=int(raw.get("total_ut_steps", 4)),
+        )
+        eos = raw.get("eos_token_id")
+        if isinstance(eos, list):
+            eos = eos[0] if eos else None
+        kw["eos_token_id"] = None if eos is None else int(eos)
+        if "init_std" in raw:
+            kw["init_std"] = float(raw["init_std"])
+        return cls(**kw)
+
 
 class RMSNorm(nn.Module):
     def __init__(self, dim: int, eps: float) -> None:
@@ -49,6 +85,12 @@ class RMSNorm(nn.Module):
         h = x.float()
         h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.eps)
         return (self.weight.float() * h).to(x.dtype)
+
+
+@dataclass
+class DenseOutput:
+    logits: torch.Tensor
+    past_key_values: None = None
 
 
 class RotaryEmbedding(nn.Module):
@@ -146,22 +188,65 @@ class OuroForCausalLM(nn.Module):
         return model.eval()
 
     def save_pretrained(self, path: str) -> None:
+        """``config.json`` (Hugging Face field names, ``model_type: ouro``) and
+        ``model.safetensors`` with the Hugging Face parameter names."""
         from safetensors.torch import save_file
 
         os.makedirs(path, exist_ok=True)
+        cfg = asdict(self.config)
+        cfg.update(model_type="ouro", architectures=["OuroForCausalLM"], tie_word_embeddings=False,
+                   layer_types=["full_attention"] * self.config.num_hidden_layers, sliding_window=None)
         with open(os.path.join(path, "config.json"), "w") as f:
-            json.dump(asdict(self.config), f, indent=1)
+            json.dump(cfg, f, indent=1)
         save_file({k: v.contiguous() for k, v in self.state_dict().items()}, os.path.join(path, "model.safetensors"))
 
     @classmethod
     def from_pretrained(cls, path: str, *, dtype=torch.bfloat16, device="cpu") -> "OuroForCausalLM":
-        """Load a directory written by ``save_pretrained`` (safetensors: no code is executed)."""
-        from safetensors.torch import load_file
+        """Load a Hugging Face-style Ouro checkpoint directory (the layout
+        ``flashloop/engine.py:134-150`` loads through ``AutoModelForCausalLM``): a
+        ``config.json`` (``OuroConfig.from_hf_config``) and the weights in
+        ``model.safetensors`` or sharded per ``model.safetensors.index.json``.  Only
+        safetensors are read (no code runs).  Parameters are matched by their Hugging Face
+        names; checkpoint tensors this model has no parameter for (e.g. early-exit gates)
+        are listed in ``unused_checkpoint_keys``; a missing parameter is an error, except
+        ``lm_head.weight`` with ``tie_word_embeddings``."""
+        from safetensors import safe_open
 
         with open(os.path.join(path, "config.json")) as f:
-            cfg = OuroConfig(**json.load(f))
+            raw = json.load(f)
+        cfg = OuroConfig.from_hf_config(raw)
+        index = os.path.join(path, "model.safetensors.index.json")
+        if os.path.exists(index):
+            with open(index) as f:
+                weight_map = json.load(f)["weight_map"]
+            files: dict[str, list[str]] = {}
+            for name, fname in weight_map.items():
+                files.setdefault(fname, []).append(name)
+        elif os.path.exists(os.path.join(path, "model.safetensors")):
+            files = {"model.safetensors": None}
+        else:
+            raise FileNotFoundError(f"{path}: neither model.safetensors nor model.safetensors.index.json")
         model = cls(cfg)
-        model.load_state_dict(load_file(os.path.join(path, "model.safetensors")))
+        wanted = model.state_dict()
+        loaded: dict[str, torch.Tensor] = {}
+        unused = []
+        for fname, names in files.items():
+            with safe_open(os.path.join(path, fname), framework="pt") as f:
+                for name in (names if names is not None else f.keys()):
+                    if name in wanted:
+                        loaded[name] = f.get_tensor(name)
+                    else:
+                        unused.append(name)
+        if "lm_head.weight" not in loaded and raw.get("tie_word_embeddings") and "model.embed_tokens.weight" in loaded:
+            loaded["lm_head.weight"] = loaded["model.embed_tokens.weight"]
+        missing = sorted(set(wanted) - set(loaded))
+        if missing:
+            raise KeyError(f"{path}: checkpoint lacks {len(missing)} parameter(s), e.g. {missing[:3]}")
+        for name, t in loaded.items():
+            if tuple(t.shape) != tuple(wanted[name].shape):
+                raise ValueError(f"{path}: {name} has shape {tuple(t.shape)}, the config implies {tuple(wanted[name].shape)}")
+        model.load_state_dict({k: v.to(torch.float32) for k, v in loaded.items()})
+        model.unused_checkpoint_keys = sorted(unused)
         return model.to(device=device, dtype=dtype).eval()
 
     # ------------------------------------------------------------------ dense reference
@@ -169,6 +254,20 @@ class OuroForCausalLM(nn.Module):
     def dense_forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         """All loops dense, no cache compression: logits of the last position (the
         looped model without FlashLoop's lazy updates)."""
+        return self.lm_head(self._dense_hidden(input_ids)[:, -1]).float()
+
+    @torch.inference_mode()
+    def forward(self, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None, **kwargs):
+        """Logits ``[1, T, vocab]`` of every position with every loop dense and no cache
+        (the model without FlashLoop).  Inside ``flashloop_amd.hooks.flashloop(model)``
+        calls are routed through ``FlashLoopEngine`` instead."""
+        if kwargs.get("past_key_values") is not None:
+            raise ValueError("the dense model keeps no cache; use flashloop(model) or FlashLoopEngine to decode")
+        if attention_mask is not None and not bool(attention_mask.bool().all()):
+            raise ValueError("padded inputs are not supported")
+        return DenseOutput(self.lm_head(self._dense_hidden(input_ids)).float())
+
+    def _dense_hidden(self, input_ids: torch.Tensor) -> torch.Tensor:
         bb = self.model
         h = bb.embed_tokens(input_ids)
         t = input_ids.shape[1]
@@ -186,7 +285,7 @@ class OuroForCausalLM(nn.Module):
                 h = h + layer.input_layernorm_2(o)
                 h = h + layer.post_attention_layernorm_2(layer.mlp(layer.post_attention_layernorm(h)))
             h = bb.norm(h)
-        return self.lm_head(h[:, -1]).float()
+        return h
 
     @torch.inference_mode()
     def generate(self, input_ids: torch.Tensor, *, max_new_tokens: int, eos_token_id: int | None = None) -> torch.Tensor:

@@ -252,3 +252,75 @@ def test_cfg4_full_model_prefill_and_decode():
         tok = torch.argmax(a.logits, dim=-1, keepdim=True)
     print(f"[parity] cfg4 worst cosine fused vs modules {worst:.6f}", flush=True)
     assert lc.quantized_tokens == 8192  # one 64-token group rolled out of the tail
+
+
+def test_hooks_route_forward_and_generate_with_observed_counters(tmp_path):
+    """Inside flashloop(model) a plain forward prefills (all positions), a forward with the
+    returned cache decodes, and generate runs the engine; the counters are what ran, and
+    the kv audit's byte fields equal the reference's formulas (oracle restatement) over
+    the rows the packed cache actually holds."""
+    from oracle import accounting as OACC
+
+    from test_model_cpu import _hf_dir
+
+    src = OuroForCausalLM.random_init(TINY, seed=11, device="cuda")
+    _hf_dir(tmp_path, src.cpu())
+    eng_ref = FlashLoopEngine.from_pretrained(str(tmp_path), device="cuda")  # HF-style sharded directory
+    model = eng_ref.model
+    ids = _ids(200, seed=11)
+    steps = 5
+    ref_pre = eng_ref.prefill(ids, decode_capacity=64)
+    tok = torch.argmax(ref_pre.logits, dim=-1, keepdim=True)
+    ref_steps = []
+    for _ in range(steps):
+        d = eng_ref.decode(tok)
+        ref_steps.append(d.logits.clone())
+        tok = torch.argmax(d.logits, dim=-1, keepdim=True)
+    with flashloop(model) as hooks:
+        out = model(ids)
+        assert out.logits.shape == (1, 200, TINY.vocab_size)
+        # the last position of an all-positions lm_head (another GEMM shape: bf16 rounding)
+        assert (out.logits[:, -1] - ref_pre.logits).abs().max().item() < 2e-2
+        assert torch.equal(torch.argmax(out.logits[:, -1], -1), torch.argmax(ref_pre.logits, -1))
+        cache = out.past_key_values
+        tok = torch.argmax(out.logits[:, -1], dim=-1, keepdim=True)
+        for i in range(steps):
+            o = model(tok, past_key_values=cache)
+            assert torch.equal(o.logits[:, 0], ref_steps[i]), f"routed decode step {i}"
+            cache = o.past_key_values
+            tok = torch.argmax(o.logits[:, 0], dim=-1, keepdim=True)
+        with pytest.raises(ValueError):
+            model(tok, past_key_values=out.past_key_values)  # stale
+        kv = hooks["kv"].audit()
+        joint = hooks["attention_and_prefill"].audit()
+        assert kv["forward_calls"] == 1 + steps and kv["cache_updates"] == 1 + steps
+        nl = TINY.num_hidden_layers
+        assert joint["attention"] == {"prefill_attention_calls": 4 * nl, "source_captures": steps * nl,
+                                      "target_replacements": 2 * steps * nl}
+        assert joint["token_sparse_prefill"] == {"active_counts": {"3": 50, "4": 20}, "mask_nested": True}
+        st = hooks["kv"].engine.state
+        m3 = st.mask_loop3.cpu().numpy()[0]
+        m4 = st.mask_loop4.cpu().numpy()[0]
+        tp = kv["quantized_tokens"]
+        groups = []
+        for _ in range(nl):
+            for g in range(tp // 64):
+                groups.append(OACC.temporal_group_bytes((1, TINY.num_attention_heads, 64, 128),
+                                                        [64, int(m3[g * 64:(g + 1) * 64].sum()),
+                                                         int(m4[g * 64:(g + 1) * 64].sum())])["packed_bytes"])
+        want = OACC.compressor_audit(num_layers=nl, recurrent_steps=4, batch=1, heads=TINY.num_attention_heads,
+                                     channels=128, total_tokens=200 + steps, current_tokens=200 + steps,
+                                     next_start=[tp] * nl, packed_stream_bytes=sum(groups),
+                                     quantized_groups=len(groups), mask_numel=200)
+        for key, value in want.items():
+            assert kv[key] == value, key
+        lay = st.cache.layers[0]
+        want_store = nl * OACC.kivi_layer_storage_bytes(
+            batch=1, heads=TINY.num_attention_heads, channels=128, packed_tokens=tp, tail_tokens=200 + steps - tp,
+            rows3=int(m3[:tp].sum()), rows4=int(m4[:tp].sum()))
+        assert kv["reference_layout_storage_bytes"] == want_store
+        assert kv["physical_storage_bytes"] == st.cache.storage_bytes
+        gen = model.generate(ids, max_new_tokens=3)
+        assert gen.shape == (1, 203)
+        assert hooks["kv"].audit()["forward_calls"] == 1 + steps + 3
+    assert lay.late_rows_host[0][0] == int(m3[:tp].sum())

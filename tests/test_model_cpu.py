@@ -67,3 +67,87 @@ def test_batch_engine_lengths_validation():
         FlashLoopBatchEngine._lengths(ids, _t.tensor([[0, 1, 1, 1, 1]] * 3))
     with _pt.raises(ValueError, match="no tokens"):
         FlashLoopBatchEngine._lengths(ids, _t.zeros(3, 5))
+
+
+def _hf_dir(tmp_path, model, *, shards=2, extra=True, tied=False):
+    """A Hugging Face-style Ouro checkpoint directory written the way HF writes one:
+    config.json with keys this build ignores, weights sharded per an index file, plus
+    tensors (early-exit gate) this model has no parameter for."""
+    import json
+
+    from safetensors.torch import save_file
+
+    cfg = dict(model.config.__dict__)
+    del cfg["head_dim"]  # HF Ouro configs may leave it implicit (hidden / heads)
+    cfg.update(model_type="ouro", architectures=["OuroForCausalLM"], torch_dtype="bfloat16",
+               max_position_embeddings=65536, hidden_act="silu", layer_types=["full_attention"] * 2,
+               sliding_window=None, tie_word_embeddings=tied, auto_map={"AutoConfig": "x.OuroConfig"},
+               eos_token_id=[2])
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    sd = {k: v.contiguous() for k, v in model.state_dict().items()}
+    if tied:
+        del sd["lm_head.weight"]
+    if extra:
+        sd["model.early_exit_gate.weight"] = torch.zeros(1, model.config.hidden_size)
+    names = sorted(sd)
+    weight_map = {}
+    for i in range(shards):
+        part = names[i::shards]
+        fname = f"model-{i + 1:05d}-of-{shards:05d}.safetensors"
+        save_file({k: sd[k] for k in part}, str(tmp_path / fname))
+        weight_map.update({k: fname for k in part})
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"metadata": {}, "weight_map": weight_map}))
+
+
+def test_from_pretrained_reads_hf_sharded_checkpoints(tmp_path):
+    a = OuroForCausalLM.random_init(TINY, seed=5)
+    _hf_dir(tmp_path, a)
+    b = OuroForCausalLM.from_pretrained(str(tmp_path))
+    assert b.config.head_dim == 128 and b.config.eos_token_id == 2
+    assert b.unused_checkpoint_keys == ["model.early_exit_gate.weight"]
+    for (ka, va), (kb, vb) in zip(a.state_dict().items(), b.state_dict().items()):
+        assert ka == kb and torch.equal(va, vb)
+
+
+def test_from_pretrained_ties_and_refusals(tmp_path):
+    import json
+
+    a = OuroForCausalLM.random_init(TINY, seed=6)
+    d1 = tmp_path / "tied"
+    d1.mkdir()
+    _hf_dir(d1, a, shards=1, tied=True)
+    b = OuroForCausalLM.from_pretrained(str(d1))
+    assert torch.equal(b.lm_head.weight, a.model.embed_tokens.weight)
+    # a variant the engine does not implement, and a checkpoint missing a parameter
+    cfg = json.loads((d1 / "config.json").read_text())
+    for bad in ({"model_type": "llama"}, {"sliding_window": 4096}, {"layer_types": ["sliding_attention"] * 2}):
+        (d1 / "config.json").write_text(json.dumps({**cfg, **bad}))
+        with pytest.raises(ValueError):
+            OuroForCausalLM.from_pretrained(str(d1))
+    (d1 / "config.json").write_text(json.dumps({**cfg, "tie_word_embeddings": False}))
+    with pytest.raises(KeyError):
+        OuroForCausalLM.from_pretrained(str(d1))
+
+
+def test_flashloop_hooks_refuse_what_they_cannot_honour():
+    from flashloop_amd.hooks import flashloop
+
+    model = OuroForCausalLM.random_init(TINY, seed=7)
+    ids = torch.randint(0, TINY.vocab_size, (1, 9), generator=torch.Generator().manual_seed(1))
+    dense = model(ids).logits
+    with flashloop(model):
+        with pytest.raises(TypeError):
+            model.generate(ids, max_new_tokens=2, temperature=0.7)
+        with pytest.raises(ValueError):
+            model.generate(ids, max_new_tokens=2, do_sample=True)
+        with pytest.raises(ValueError):
+            model.generate(ids, max_new_tokens=2, num_beams=4)
+        with pytest.raises(ValueError):
+            model.generate(ids, max_new_tokens=2, attention_mask=torch.tensor([[0] + [1] * 8]))
+        with pytest.raises(TypeError):
+            model(ids, output_attentions=True)
+        with pytest.raises(TypeError):
+            model(ids[:, :1], past_key_values=object())
+    # restored on exit: the dense model again
+    assert "forward" not in model.__dict__ and "generate" not in model.__dict__
+    assert torch.equal(model(ids).logits, dense)
