@@ -178,7 +178,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(the path shards by (batch, head) with no exchange; see DESIGN.md)"}))
+                                   "(the path would shard by (batch, head) rows, with no exchange between GPUs)"}))
         sys.exit(2)
     if args.config == "cfg4":
         bench_cfg4(args)

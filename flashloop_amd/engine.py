@@ -109,6 +109,7 @@ class DecodeRunner:
         self.engine = engine
         self.use_graphs = bool(use_graphs)
         self.graph = None
+        self.captures = 0  # graphs captured so far
         self.reset()
 
     def _release(self) -> None:
@@ -173,6 +174,7 @@ class DecodeRunner:
             self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
             self.out.copy_(self.logits)
         self.graph = graph
+        self.captures += 1
 
 
 class FlashLoopEngine:

@@ -191,13 +191,13 @@ def test_graph_recapture_releases_old_graphs():
     ids = _ids(400, seed=10)
     eng.prefill(ids[:, :200], decode_capacity=256)
     held = []
-    graphs = set()
+    first = None
     for i in range(200, 330):  # fraction 1: the selection capacity steps every 64 keys
         out = eng.decode(ids[:, i:i + 1])
         held.append(out)  # outputs held across recaptures stay valid tensors
-        graphs.add(id(eng._runner.graph))
+        first = eng._runner.captures if first is None else first
         gc.collect()
-    assert len(graphs) >= 3
+    assert eng._runner.captures - first >= 2
     assert all(torch.isfinite(o.logits).all() for o in held[-3:])
 
 
