@@ -23,9 +23,10 @@ constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / kWave;
 
 // Order-preserving unsigned key of a score.  -0.0 takes the key of +0.0 (they compare
-// equal, so the lower index wins their tie, as in torch.topk and a stable sort).
+// equal, so the lower index wins their tie, as in torch.topk and a stable sort): adding
+// +0.0 maps -0.0 to +0.0 and leaves every other value (NaN included) as it is.
 __device__ __forceinline__ uint32_t order_key(float f) {
-  const uint32_t u = f == 0.0f ? 0u : __float_as_uint(f);
+  const uint32_t u = __float_as_uint(f + 0.0f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 // NaN or +-inf (flashloop/selection.py:78-79 rejects such weights)
@@ -296,6 +297,7 @@ struct ResShared {
   uint32_t kth_idx;
   uint32_t total;
   uint32_t nonfin;
+  uint32_t badrow;
 };
 
 __device__ float res_block_max(float v, ResShared& sh) {
@@ -401,8 +403,11 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   // needs an index test.
   uint32_t kr[PER];
   float mx = -INFINITY, mn = INFINITY;
-  uint32_t nf = 0;  // non-finite keys of this wave (wave-uniform)
-  if (tid == 0) sh.nonfin = 0;
+  if (tid == 0) {
+    sh.nonfin = 0;
+    sh.badrow = 0;
+  }
+  float chk = 0.0f;  // x*0 summed: 0 unless some score is NaN or +-inf
   {
     float xs[PER];
 #pragma unroll
@@ -414,7 +419,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
     for (int j = 0; j < PER; ++j) {
       const bool in = j * kTopkThreads + tid < n;
       kr[j] = in ? max(order_key(xs[j]), kPadKey + 1u) : kPadKey;
-      nf += static_cast<uint32_t>(__popcll(ballot64(in && non_finite(xs[j]))));
+      chk = fmaf(xs[j], 0.0f, chk);  // (xs[j] is 0 past n)
       if (in) {
         mx = fmaxf(mx, xs[j]);
         mn = fminf(mn, xs[j]);
@@ -423,9 +428,10 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   }
   for (int i = tid; i < kBins; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
   if (tid == 0) sh.ncand = 0;
-  const float M = res_block_max(mx, sh);  // (its barriers order the counter's reset)
-  if (lane == 0 && nf) atomicAdd(&sh.nonfin, nf);
-  mn = -res_block_max(-mn, sh);
+  const float M = res_block_max(mx, sh);  // (its barriers order the flag's reset)
+  if (chk != 0.0f) sh.badrow = 1u;
+  mn = -res_block_max(-mn, sh);           // (its barriers publish the flag)
+  const bool badrow = sh.badrow != 0u;
   // bin(x) = clamp(x * inv - mn * inv); non-finite extremes collapse every key into bin 0
   // (the crowded-bin fallback then covers all)
   const float inv = (isfinite(M) && isfinite(mn) && M > mn) ? static_cast<float>(kBins) / (M - mn) : 0.0f;
@@ -442,6 +448,13 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
     atomicAdd(&lin[value_bin(xi, inv, off)], 1u);
   }
   const float Z = res_block_sum(z, sh);  // (its barriers also complete the histogram)
+  // Only a row holding a non-finite score (the same decision in every thread) counts
+  // them, re-reading the row.
+  if (badrow) {
+    uint32_t c = 0;
+    for (int i = tid; i < n; i += kTopkThreads) c += non_finite(x[i]) ? 1u : 0u;
+    if (c) atomicAdd(&sh.nonfin, c);
+  }
   {
     const int bin = kBins - 1 - tid;  // descending scan: thread t owns bin kBins-1-t
     const uint32_t h = lin[bin] - (bin == 0 ? static_cast<uint32_t>(PER * kTopkThreads - n) : 0u);

@@ -581,17 +581,21 @@ def test_topk_signed_zeros_tie(n):
 def test_topk_reports_non_finite_scores(n):
     print("case: topk non-finite n=%d" % n, flush=True)
     rng = np.random.default_rng(9)
-    lg = rng.standard_normal((3, n)).astype(np.float32)
+    lg = rng.standard_normal((5, n)).astype(np.float32)
+    neg_nan = np.array([0xFFC00000], dtype=np.uint32).view(np.float32)[0]  # NaN with the sign bit set
     lg[1, 5] = np.nan
     lg[2, 7] = np.inf
     lg[2, 9] = -np.inf
-    nk = torch.full((3,), n, dtype=torch.int32, device=DEV)
+    lg[3, 11] = neg_nan
+    lg[4, [0, n - 1]] = np.nan
+    lg[4, 100] = neg_nan
+    nk = torch.full((5,), n, dtype=torch.int32, device=DEV)
     cap = OA.padded_capacity(OA.decode_budget(n, 0.1))
-    nf = torch.full((3,), -1, dtype=torch.int32, device=DEV)
+    nf = torch.full((5,), -1, dtype=torch.int32, device=DEV)
     t = torch.from_numpy(lg).to(DEV)
     kernels.decode_topk(t, nk, 0.1, cap, nonfinite=nf)
     torch.cuda.synchronize()
-    assert nf.cpu().tolist() == [0, 1, 2]
+    assert nf.cpu().tolist() == [0, 1, 2, 1, 3]
     with pytest.raises(ValueError):
         kernels.decode_topk(t, nk, 0.1, cap, validate=True)
     kernels.decode_topk(t[:1], nk[:1], 0.1, cap, validate=True)  # finite row passes
