@@ -428,6 +428,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         L.qf[2 * lane + 1] = bf16hi_to_f32(T.qw) * a.scaling;
       }
     }
+#ifdef FL_GATHER_NOCOMPUTE
+    // Measurement build only (never the default): the tile's arithmetic is replaced by
+    // folding every loaded word into one register, so a run of this build times the
+    // access pattern and pipeline alone.  Outputs are meaningless.
+    {
+      uint32_t x = T.qw ^ __float_as_uint(T.vm01.x) ^ __float_as_uint(T.vm23.y) ^ static_cast<uint32_t>(T.t);
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) x ^= T.kw[s][k] ^ T.vw[s][k];
+      if (kSoftmax)
+#pragma unroll
+        for (int j = 0; j < kNew; ++j)
+          if (j < T.nnew)
+#pragma unroll
+            for (int s = 0; s < NS; ++s) x ^= T.km[j][s].x ^ T.km[j][s].y;
+      o.acc[0] += static_cast<float>(x & 7u);
+      o.l += 1.0f;
+      return;
+    }
+#endif
     const int t = T.t, Tp = T.Tp, cur = T.cur;
     const uint32_t has = T.has;
     const bool pre = t >= 0 && t < Tp;
@@ -727,7 +748,11 @@ constexpr int kLpt = FL_GATHER_LPT;  // lanes per selected slot
 
 template <int NS, int MODE>
 void launch_ns(GatherArgs& a, int rows, hipStream_t st) {
+#ifdef FL_GATHER_OCC  // measurement build only: resident workgroups per CU forced
+  const int blocks = gather_blocks(rows, a.cap, FL_GATHER_OCC);
+#else
   const int blocks = gather_blocks(rows, a.cap, gather_occupancy<NS, MODE, kLpt>());
+#endif
   a.waves = blocks * kWaves;
   a.tpr = a.cap / Lay<kLpt>::kTok;
   hipLaunchKernelGGL((gather_reader_kernel<NS, MODE, kLpt>), dim3(blocks), dim3(kThreads), 0, st, a);
