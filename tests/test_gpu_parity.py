@@ -24,6 +24,7 @@ from gpu_util import (
     materialized,
     np32,
     oracle_prefix,
+    restated_dense_logits,
 )
 
 pytestmark = pytest.mark.gpu
@@ -156,6 +157,12 @@ def test_dense_reader_all_loops(masked):
         assert_close(np32(out).reshape(6, 128), want, what=f"loop {loop} output")
         got_lg = np32(logits).reshape(6, -1)
         assert got_lg.shape[1] >= want_lg.shape[1] and got_lg.shape[1] % 64 == 0  # padded, aligned row stride
+        # two bars: the kernel's contraction against an fp64 restatement of its own
+        # arithmetic (tight), and against the oracle's bf16 chain, whose per-stream
+        # re-rounding the reader skips (~2e-3 on logits)
+        rest = restated_dense_logits(layer, loop, range(6), q, np32(kc).reshape(6, 128), SCALING)
+        assert_close(got_lg[:, : want_lg.shape[1]], np.stack(rest), max_abs=1e-4, mean_abs=1e-5,
+                     what=f"loop {loop} logits vs restated reader arithmetic")
         assert_close(got_lg[:, : want_lg.shape[1]], want_lg, max_abs=2e-2, mean_abs=5e-3, what=f"loop {loop} logits")
 
 
