@@ -289,7 +289,10 @@ struct ResShared {
   uint32_t cand_rank[kCand];
   uint32_t sel_idx[kSelLds];
   uint32_t sel_key[kSelLds];
+  uint16_t bin[kPer][kTopkThreads];  // value bin of each key (pass 2), read by pass 3
   float red[kTopkWaves];
+  float red2[kTopkWaves];
+  float red3[kTopkWaves];
   uint32_t sel_digit;
   uint32_t bin_above;
   uint32_t ncand;
@@ -297,7 +300,6 @@ struct ResShared {
   uint32_t kth_idx;
   uint32_t total;
   uint32_t nonfin;
-  uint32_t badrow;
 };
 
 __device__ float res_block_max(float v, ResShared& sh) {
@@ -308,6 +310,28 @@ __device__ float res_block_max(float v, ResShared& sh) {
   float r = sh.red[0];
 #pragma unroll
   for (int i = 1; i < kTopkWaves; ++i) r = fmaxf(r, sh.red[i]);
+  return r;
+}
+
+// max over the workgroup of a, of b and of c, in one exchange
+__device__ float3 res_block_max3(float a, float b, float c, ResShared& sh) {
+  a = wave_max(a);
+  b = wave_max(b);
+  c = wave_max(c);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    sh.red[threadIdx.x >> 6] = a;
+    sh.red2[threadIdx.x >> 6] = b;
+    sh.red3[threadIdx.x >> 6] = c;
+  }
+  __syncthreads();
+  float3 r = make_float3(sh.red[0], sh.red2[0], sh.red3[0]);
+#pragma unroll
+  for (int i = 1; i < kTopkWaves; ++i) {
+    r.x = fmaxf(r.x, sh.red[i]);
+    r.y = fmaxf(r.y, sh.red2[i]);
+    r.z = fmaxf(r.z, sh.red3[i]);
+  }
   return r;
 }
 
@@ -403,10 +427,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   // needs an index test.
   uint32_t kr[PER];
   float mx = -INFINITY, mn = INFINITY;
-  if (tid == 0) {
-    sh.nonfin = 0;
-    sh.badrow = 0;
-  }
+  if (tid == 0) sh.nonfin = 0;
   float chk = 0.0f;  // x*0 summed: 0 unless some score is NaN or +-inf
   {
     float xs[PER];
@@ -428,10 +449,10 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   }
   for (int i = tid; i < kBins; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
   if (tid == 0) sh.ncand = 0;
-  const float M = res_block_max(mx, sh);  // (its barriers order the flag's reset)
-  if (chk != 0.0f) sh.badrow = 1u;
-  mn = -res_block_max(-mn, sh);           // (its barriers publish the flag)
-  const bool badrow = sh.badrow != 0u;
+  const float3 ext = res_block_max3(mx, -mn, chk != 0.0f ? 1.0f : 0.0f, sh);  // (its barriers order the reset)
+  const float M = ext.x;
+  mn = -ext.y;
+  const bool badrow = ext.z != 0.0f;
   // bin(x) = clamp(x * inv - mn * inv); non-finite extremes collapse every key into bin 0
   // (the crowded-bin fallback then covers all)
   const float inv = (isfinite(M) && isfinite(mn) && M > mn) ? static_cast<float>(kBins) / (M - mn) : 0.0f;
@@ -445,7 +466,9 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   for (int j = 0; j < PER; ++j) {
     const float xi = key_value(kr[j]);
     z += fast_exp2(fmaf(xi, kLog2e, -mlog));
-    atomicAdd(&lin[value_bin(xi, inv, off)], 1u);
+    const int b = value_bin(xi, inv, off);
+    sh.bin[j][tid] = static_cast<uint16_t>(b);
+    atomicAdd(&lin[b], 1u);
   }
   const float Z = res_block_sum(z, sh);  // (its barriers also complete the histogram)
   // Only a row holding a non-finite score (the same decision in every thread) counts
@@ -483,7 +506,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int i = j * kTopkThreads + tid;
-    const int b = value_bin(key_value(kr[j]), inv, off);
+    const int b = sh.bin[j][tid];
     const uint64_t bal_a = ballot64(b > bstar);
     const bool in_b = b == bstar && kr[j] != kPadKey;
     const uint64_t bal_b = ballot64(in_b);
@@ -546,7 +569,7 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         const uint32_t kk = kr[j];
-        if (kk != kPadKey && (kk & pmask) == prefix && value_bin(key_value(kk), inv, off) == bstar)
+        if (kk != kPadKey && (kk & pmask) == prefix && static_cast<int>(sh.bin[j][tid]) == bstar)
           atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
       }
       __syncthreads();
