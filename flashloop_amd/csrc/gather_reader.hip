@@ -471,8 +471,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       auto stage_group = [&](uint2 km, float* qs, float* qm) {
         const float sc0 = f16_to_f32(km.x & 0xFFFFu), mn0 = f16_to_f32(km.x >> 16);
         const float sc1 = f16_to_f32(km.y & 0xFFFFu), mn1 = f16_to_f32(km.y >> 16);
-        qs[2 * lane] = q0 * sc0;
-        qs[2 * lane + 1] = q1 * sc1 * 0.0625f;  // high nibbles read as 16*code
+        qs[2 * lane] = (q0 * kSub16) * sc0;  // codes read as fp16 subnormals (dot8h)
+        qs[2 * lane + 1] = (q1 * (kSub16 * 0.0625f)) * sc1;  // high nibbles read as 16*code
         float m = fmaf(q0, mn0, q1 * mn1);
         m += dpp<kDppXor1>(m);
         m += dpp<kDppXor2>(m);
@@ -492,8 +492,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           for (int k = 0; k < kWords; ++k) {
             const float4 x = *reinterpret_cast<const float4*>(qq + 8 * k);
             const float4 y = *reinterpret_cast<const float4*>(qq + 8 * k + 4);
-            const float qe[4] = {x.x, x.z, y.x, y.z}, qo[4] = {x.y, x.w, y.y, y.w};
-            e = dot8(T.kw[s][k], qe, qo, e);
+            const float qw[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+            e = dot8h(T.kw[s][k], qw, e);
           }
           d += e + qm[s][part];
         }
@@ -564,15 +564,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         if (!((has >> s) & 1u)) continue;
-        const float we = p * vm[s].x;
+        const float we = (p * kSub16) * vm[s].x;  // codes read as fp16 subnormals (axpy8h)
         o.mu = fmaf(p, vm[s].y, o.mu);
 #pragma unroll
-        for (int k = 0; k < kWords; ++k) axpy8(T.vw[s][k], we, we * 0.0625f, o.acc + 8 * k);
+        for (int k = 0; k < kWords; ++k) axpy8h(T.vw[s][k], we, we * 0.0625f, o.acc + 8 * k);
         if (kSource && s < 2) {
-          const float ws1 = w1 * vm[s].x;
+          const float ws1 = (w1 * kSub16) * vm[s].x;
           o.mu1 = fmaf(w1, vm[s].y, o.mu1);
 #pragma unroll
-          for (int k = 0; k < kWords; ++k) axpy8(T.vw[s][k], ws1, ws1 * 0.0625f, o.acc1 + 8 * k);
+          for (int k = 0; k < kWords; ++k) axpy8h(T.vw[s][k], ws1, ws1 * 0.0625f, o.acc1 + 8 * k);
         }
       }
     }

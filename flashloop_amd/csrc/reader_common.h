@@ -57,6 +57,47 @@ __device__ __forceinline__ void axpy8(uint32_t w, float we, float wo, float* acc
   acc[7] = fmaf(wo, ubyte3(hi), acc[7]);
 }
 
+// The same two contractions with the codes read as fp16 subnormals: masking a word with
+// 0x000F000F (0x00F000F0) leaves in each 16-bit half one nibble c (16c) below bit 10, the
+// fp16 value c*2^-24 (16c*2^-24), which v_fma_mix_f32 takes as an exact fp32 operand.
+// Two masks per four codes replace four conversions; the factors carry the 2^24 (and the
+// odd channels' 1/16).  q[0..7]: factors of channels 0..7 of the word.
+__device__ __forceinline__ float h16lo(uint32_t x) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x & 0xFFFFu)));
+}
+__device__ __forceinline__ float h16hi(uint32_t x) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x >> 16)));
+}
+__device__ __forceinline__ float dot8h(uint32_t w, const float* q, float acc) {
+  const uint32_t x0 = w & 0x000F000Fu, x1 = w & 0x00F000F0u;
+  const uint32_t w8 = w >> 8;
+  const uint32_t x2 = w8 & 0x000F000Fu, x3 = w8 & 0x00F000F0u;
+  acc = fmaf(q[0], h16lo(x0), acc);
+  acc = fmaf(q[4], h16hi(x0), acc);
+  acc = fmaf(q[1], h16lo(x1), acc);
+  acc = fmaf(q[5], h16hi(x1), acc);
+  acc = fmaf(q[2], h16lo(x2), acc);
+  acc = fmaf(q[6], h16hi(x2), acc);
+  acc = fmaf(q[3], h16lo(x3), acc);
+  acc = fmaf(q[7], h16hi(x3), acc);
+  return acc;
+}
+// acc[c] += we*code_c for even channels, wo*(16*code_c) for odd ones (we, wo scaled by 2^24)
+__device__ __forceinline__ void axpy8h(uint32_t w, float we, float wo, float* acc) {
+  const uint32_t x0 = w & 0x000F000Fu, x1 = w & 0x00F000F0u;
+  const uint32_t w8 = w >> 8;
+  const uint32_t x2 = w8 & 0x000F000Fu, x3 = w8 & 0x00F000F0u;
+  acc[0] = fmaf(we, h16lo(x0), acc[0]);
+  acc[4] = fmaf(we, h16hi(x0), acc[4]);
+  acc[1] = fmaf(wo, h16lo(x1), acc[1]);
+  acc[5] = fmaf(wo, h16hi(x1), acc[5]);
+  acc[2] = fmaf(we, h16lo(x2), acc[2]);
+  acc[6] = fmaf(we, h16hi(x2), acc[6]);
+  acc[3] = fmaf(wo, h16lo(x3), acc[3]);
+  acc[7] = fmaf(wo, h16hi(x3), acc[7]);
+}
+constexpr float kSub16 = 16777216.0f;  // 2^24: fp16 subnormal code c reads as c * 2^-24
+
 struct QuadState {
   float m, l, mu;
   float acc[32];
