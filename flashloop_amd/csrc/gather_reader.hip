@@ -544,9 +544,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       }
       d = slot_sum<LPT>(d);
       lg = t >= 0 ? d : -INFINITY;
-      // online softmax over the wave's slots (m wave-uniform, rescaled lazily)
-      const float tmax = wave_max(lg);
-      if (tmax > o.m + 8.0f) {
+      // online softmax over the wave's slots (m wave-uniform, rescaled lazily); the
+      // wave's maximum is formed only when some slot exceeds m by more than e^8
+      if (__ballot(lg > o.m + 8.0f)) {
+        const float tmax = wave_max(lg);
         const float alpha = o.m == -INFINITY ? 0.0f : fast_exp2((o.m - tmax) * kLog2e);
         o.l *= alpha;
         o.mu *= alpha;
