@@ -485,7 +485,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         float d = 0.0f;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          if (!((has >> s) & 1u)) continue;
+          // streams 0/1 hold every prefix token; stream 2 is selected, not branched over
+          // (an absent row reads row 0's codes, which the select discards); stream 3 is
+          // branched over (selecting it too costs the loop-4 kernel registers it spills)
+          if (s == 3 && !((has >> s) & 1u)) continue;
           const float* qq = &qs[s][kCh * part];
           float e = 0.0f;
 #pragma unroll
@@ -495,7 +498,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             const float qw[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
             e = dot8h(T.kw[s][k], qw, e);
           }
-          d += e + qm[s][part];
+          const float t = e + qm[s][part];
+          d += (s != 2 || ((has >> s) & 1u)) ? t : 0.0f;
         }
         return d;
       };
@@ -564,9 +568,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     if (pre) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        if (!((has >> s) & 1u)) continue;
-        const float we = (p * kSub16) * vm[s].x;  // codes read as fp16 subnormals (axpy8h)
-        o.mu = fmaf(p, vm[s].y, o.mu);
+        // an absent stream-2 row (row 0's codes were read) gets weight 0 by a select;
+        // stream 3 is branched over
+        if (s == 3 && !((has >> s) & 1u)) continue;
+        const bool in = s != 2 || ((has >> s) & 1u);
+        const float we = in ? (p * kSub16) * vm[s].x : 0.0f;  // codes read as fp16 subnormals (axpy8h)
+        o.mu += in ? p * vm[s].y : 0.0f;
 #pragma unroll
         for (int k = 0; k < kWords; ++k) axpy8h(T.vw[s][k], we, we * 0.0625f, o.acc + 8 * k);
         if (kSource && s < 2) {
