@@ -323,8 +323,9 @@ __device__ __forceinline__ void compute_group(const GroupSet<NS>& gs, WaveState&
   // ---- softmax of the lane's own token (row = lane: tile `quarter`, position n)
   const float lgo = quarter == 0 ? lg[0] : quarter == 1 ? lg[1] : quarter == 2 ? lg[2] : lg[3];
   if (LOGITS) lgbuf[lane] = lgo;  // staged; written out in batches (see flush_logits)
-  const float gmax = wave_max(lgo);
-  if (gmax > st.m + kLazyRescale) {  // wave-uniform
+  // the wave's maximum is formed only when some token exceeds m by more than e^8
+  if (__ballot(lgo > st.m + kLazyRescale)) {  // wave-uniform
+    const float gmax = wave_max(lgo);
     const float alpha = st.m == -INFINITY ? 0.0f : fast_exp2((st.m - gmax) * kLog2e);
     st.l *= alpha;
     st.mu0 *= alpha;
