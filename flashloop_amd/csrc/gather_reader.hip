@@ -363,14 +363,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       // row base (scalar) + line offset (32-bit: row < row_capacity < 2^24)
       const int64_t base = static_cast<int64_t>(sl.bh) * v.row_capacity[s] * kCodeStride;
       const uint32_t off = static_cast<uint32_t>(row[s]) * kCodeStride + 4 * kWords * part;
+#ifdef FL_GATHER_NOLOAD
+      // measurement build only: the code words come from the slot's token instead of
+      // memory (index and rank loads stay), so a run times the arithmetic's chains
+      for (int k = 0; k < kWords; ++k) {
+        T.kw[s][k] = static_cast<uint32_t>(sl.t) * 2654435761u + 97u * s + 13u * k + off;
+        T.vw[s][k] = static_cast<uint32_t>(sl.t) * 40503u + 31u * s + 7u * k + off;
+      }
+      (void)base;
+#else
       if (kSoftmax) load_words<LPT>(T.kw[s], v.key_codes[s] + base + off);
       load_words<LPT>(T.vw[s], v.value_codes[s] + base + off);
+#endif
     }
     // V metadata of every stream from the token's 64-byte record (this lane's half: 32 bytes)
     const float* rec = v.value_meta_token + static_cast<int64_t>(sl.bh) * v.token_capacity * 16;
     const uint32_t roff = static_cast<uint32_t>(pre ? sl.t : 0) * 64u + half * 32u;
+#ifdef FL_GATHER_NOLOAD
+    {
+      const float f = static_cast<float>(roff & 1023u) * 1e-4f;
+      T.vm01 = make_float4(0.01f + f, f, 0.02f + f, f);
+      T.vm23 = make_float4(0.03f + f, f, 0.04f + f, f);
+      (void)rec;
+    }
+#else
     T.vm01 = load_at<float4>(rec, roff);
     T.vm23 = NS > 2 ? load_at<float4>(rec, roff + 16u) : make_float4(0.f, 0.f, 0.f, 0.f);
+#endif
     T.glo = 0;
     T.nnew = 0;
     T.gfirst = 0;
@@ -396,8 +415,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         if (j < T.nnew)
 #pragma unroll
           for (int s = 0; s < NS; ++s)
+#ifdef FL_GATHER_NOLOAD
+            T.km[j][s] = make_uint2(0x2C003C00u + static_cast<uint32_t>(T.glo + j + s) * 3u, 0x1C00u + lane);
+#else
             T.km[j][s] = load_at<uint2>(v.key_meta_half[s] + (static_cast<int64_t>(sl.bh) * gcap + T.glo + j) * kDim * 2,
                                         8u * lane);
+#endif
       T.qw = load_at<uint32_t>(a.q + static_cast<int64_t>(sl.bh) * kDim, 4u * lane);
     }
     return T;
