@@ -54,7 +54,8 @@ def parse():
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-rows", type=int, default=32, help="(b,h) rows of the CPU baseline sample (0 = skip)")
     ap.add_argument("--breakdown-steps", type=int, default=10,
-                    help="extra steps after the timed region that time each op with HIP events (0 = skip)")
+                    help="after the timed region, each op runs this many times back to back between two "
+                         "HIP events (its per-op time in the breakdown; 0 = skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline: repeat the sample's step until this much CPU time has run")
     ap.add_argument("--eager", action="store_true", help="cfg4: eager decode launches instead of HIP-graph replay")
@@ -233,37 +234,23 @@ def main():
 
     lib = _lib.load()
 
-    def timed_step(i, ev=None):
-        """One step; with ``ev`` (a list) a HIP event is recorded on the launch stream
-        before the first op and after each op (the per-op breakdown)."""
-
-        def mark():
-            if ev is not None:
-                e = torch.cuda.Event(enable_timing=True)
-                e.record()
-                ev.append(e)
-
-        mark()
+    def timed_step(i):
+        """One step, op by op (the same launches as ``step``)."""
         if (not args.paired_dense):
             out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=kcur[0], current_value=vcur[0],
                                                    scaling=SCALING, return_logits=False)
-            mark()
             out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=kcur[1],
                                                         current_value=vcur[1], scaling=SCALING, return_logits=True)
         else:
             out0, out1, logits = layer.dense_source_attention_pair(
                 queries=queries[:2], current_keys=kcur[:2], current_values=vcur[:2], scaling=SCALING)
-        mark()
         idx, valid, mass, wts, counts = layer.select_decode_keys(logits, args.fraction)
-        mark()
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
             source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)
-        mark()
         d3 = layer.cached_mass_sparse_attention_delta(3, query=queries[3], current_key=kcur[3], current_value=vcur[3],
                                                       indices=idx, valid=valid, source_selected_output=so,
                                                       global_mass=mass, scaling=SCALING)
-        mark()
         return out0, out1, d2, d3
 
     for _ in range(args.warmup):
@@ -306,26 +293,53 @@ def main():
     reader_gbps = reader_bytes / (reader_ms * 1e-3) / 1e9
     finite = all(bool(torch.isfinite(t).all()) for t in (ref.out0, ref.out1, ref.delta2, ref.delta3))
 
-    # per-op breakdown: extra steps after the timed region, events between the ops
+    # per-op breakdown after the timed region: each op of the step (its reader and merge
+    # launches) runs `breakdown_steps` times back to back on the step's inputs between two
+    # events on the launch stream, so the event overhead is paid once per op, not per run
     breakdown = None
     if args.breakdown_steps > 0:
-        names = (["dense_loop1", "dense_loop2"] if not args.paired_dense else ["dense_loop1+2"]) + \
-            ["topk", "sparse_loop3_with_source", "sparse_loop4"]
-        evs = []
-        for i in range(args.breakdown_steps):
-            ev = []
-            timed_step(i, ev)
-            evs.append(ev)
-        torch.cuda.synchronize()
+        idx, valid, mass, wts, _ = layer.select_decode_keys(ref.logits1, args.fraction)
+        so = ref.selected_output
+        ops = []
+        if not args.paired_dense:
+            ops.append(("dense_loop1", lambda: layer.dense_source_attention(
+                0, query=queries[0], current_key=kcur[0], current_value=vcur[0], scaling=SCALING,
+                return_logits=False)))
+            ops.append(("dense_loop2", lambda: layer.dense_source_attention(
+                1, query=queries[1], current_key=kcur[1], current_value=vcur[1], scaling=SCALING,
+                return_logits=True)))
+        else:
+            ops.append(("dense_loop1+2", lambda: layer.dense_source_attention_pair(
+                queries=queries[:2], current_keys=kcur[:2], current_values=vcur[:2], scaling=SCALING)))
+        ops.append(("topk", lambda: layer.select_decode_keys(ref.logits1, args.fraction)))
+        ops.append(("sparse_loop3_with_source", lambda: layer.cached_mass_sparse_attention_delta_with_source(
+            2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
+            source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)))
+        ops.append(("sparse_loop4", lambda: layer.cached_mass_sparse_attention_delta(
+            3, query=queries[3], current_key=kcur[3], current_value=vcur[3], indices=idx, valid=valid,
+            source_selected_output=so, global_mass=mass, scaling=SCALING)))
         breakdown = {}
-        for j, name in enumerate(names):
-            us = sum(ev[j].elapsed_time(ev[j + 1]) for ev in evs) / len(evs) * 1e3
+        for name, fn in ops:
+            fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            # a spin kernel first keeps the GPU busy while the host enqueues the runs, so the
+            # runs execute back to back (their host-side argument handling stays hidden, as
+            # it is inside a step)
+            torch.cuda._sleep(int(4e6))
+            e0.record()
+            for _ in range(args.breakdown_steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / args.breakdown_steps * 1e3
             nbytes = parts[name] if name in parts else parts["dense_loop1"] + parts["dense_loop2"]
             ach = nbytes / (us * 1e-6) / 1e9
             breakdown[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes, "GB_per_s": round(ach, 1),
                                "frac": round(ach / HBM_PEAK_GBPS, 4)}
-        breakdown["note"] = ("HIP events between the ops of extra steps: an op's time holds its reader, its merge "
-                             "and the launch gaps the events add; per-kernel times are in the rocprof summary")
+        breakdown["note"] = (f"each op {args.breakdown_steps} times back to back (queued behind a spin kernel) "
+                             "between two events on the launch stream: an op's time holds its reader and merge "
+                             "launches (repeats of a sparse op can find part of its 0.3-0.4 GB in the 256 MB memory-side cache); "
+                             "per-kernel times are in the rocprof summary")
 
     cpu = None
     if sample is not None:
