@@ -239,12 +239,13 @@ def main():
         if (not args.paired_dense):
             out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=kcur[0], current_value=vcur[0],
                                                    scaling=SCALING, return_logits=False)
-            out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=kcur[1],
-                                                        current_value=vcur[1], scaling=SCALING, return_logits=True)
+            out1, logits, (idx, valid, mass, wts, counts) = layer.dense_source_attention_select(
+                1, query=queries[1], current_key=kcur[1], current_value=vcur[1], scaling=SCALING,
+                fraction=args.fraction)
         else:
             out0, out1, logits = layer.dense_source_attention_pair(
                 queries=queries[:2], current_keys=kcur[:2], current_values=vcur[:2], scaling=SCALING)
-        idx, valid, mass, wts, counts = layer.select_decode_keys(logits, args.fraction)
+            idx, valid, mass, wts, counts = layer.select_decode_keys(logits, args.fraction)
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
             source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)
@@ -305,13 +306,13 @@ def main():
             ops.append(("dense_loop1", lambda: layer.dense_source_attention(
                 0, query=queries[0], current_key=kcur[0], current_value=vcur[0], scaling=SCALING,
                 return_logits=False)))
-            ops.append(("dense_loop2", lambda: layer.dense_source_attention(
+            ops.append(("dense_loop2+topk", lambda: layer.dense_source_attention_select(
                 1, query=queries[1], current_key=kcur[1], current_value=vcur[1], scaling=SCALING,
-                return_logits=True)))
+                fraction=args.fraction)))
         else:
             ops.append(("dense_loop1+2", lambda: layer.dense_source_attention_pair(
                 queries=queries[:2], current_keys=kcur[:2], current_values=vcur[:2], scaling=SCALING)))
-        ops.append(("topk", lambda: layer.select_decode_keys(ref.logits1, args.fraction)))
+            ops.append(("topk", lambda: layer.select_decode_keys(ref.logits1, args.fraction)))
         ops.append(("sparse_loop3_with_source", lambda: layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
             source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)))
@@ -332,7 +333,8 @@ def main():
             e1.record()
             torch.cuda.synchronize()
             us = e0.elapsed_time(e1) / args.breakdown_steps * 1e3
-            nbytes = parts[name] if name in parts else parts["dense_loop1"] + parts["dense_loop2"]
+            nbytes = parts[name] if name in parts else (
+                parts["dense_loop2"] + parts["topk"] if name == "dense_loop2+topk" else parts["dense_loop1"] + parts["dense_loop2"])
             ach = nbytes / (us * 1e-6) / 1e9
             breakdown[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes, "GB_per_s": round(ach, 1),
                                "frac": round(ach / HBM_PEAK_GBPS, 4)}

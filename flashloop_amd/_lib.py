@@ -72,6 +72,8 @@ SIGNATURES = {
     "fl_profile_dense_reader": (_I32, [_I32, _I32]),
     "fl_profile_dense_reader_read": (_I32, [C.POINTER(_F32), C.POINTER(_I32)]),
     "fl_decode_topk": (_I32, [_P, _I64, _I32, _P, _I32, _F64, _I32, _P, _P, _P, _P, _P, _P, _P]),
+    "fl_decode_attn_dense_select": (_I32, [_VIEW, _I32, _P, _P, _P, _F32, _P, _P, _I64, _F64, _I32, _P, _P, _P, _P,
+                                           _P, _P, _P, _SZ, _P]),
     "fl_decode_selected_workspace": (_SZ, [_VIEW, _I32]),
     "fl_decode_selected_pv": (_I32, [_VIEW, _I32, _P, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
     "fl_decode_attn_sparse_delta": (

@@ -272,6 +272,26 @@ class CrossLoopKVLayer:
         shape = (self.batch, self.heads, 1, HEAD_DIM)
         return out0.view(shape), out1.view(shape), logits.view(self.batch, self.heads, 1, -1)
 
+    def dense_source_attention_select(self, loop: int, *, query, current_key, current_value, scaling: float,
+                                      fraction: float):
+        """``dense_source_attention(loop, ..., return_logits=True)`` followed by
+        ``select_decode_keys(logits, fraction)`` (flashloop/engine.py:438-498), with the
+        read's merge and the top-k in one launch when the row stride allows it
+        (``fl_decode_attn_dense_select``).  Returns ``(out, logits, (indices, valid, mass,
+        selected_weights, counts))`` shaped as the two methods return them."""
+        cap = kernels.decode_capacity(self.token_count + 1, fraction)
+        lcap = self.logits_capacity()
+        if not kernels.dense_select_fits(lcap, fraction):
+            out, logits = self.dense_source_attention(loop, query=query, current_key=current_key,
+                                                      current_value=current_value, scaling=scaling, return_logits=True)
+            return out, logits, self.select_decode_keys(logits, fraction)
+        out, logits, idx, valid, mass, w, counts = kernels.fused_dense_select(
+            self.view(), int(loop), query, current_key, current_value, scaling, fraction, cap,
+            logits_capacity=lcap, device=self.device, workspace=self.workspace)
+        shape = (self.batch, self.heads, cap)
+        return (out.view(self.batch, self.heads, 1, HEAD_DIM), logits.view(self.batch, self.heads, 1, -1),
+                (idx.view(shape), valid.view(shape), mass.view(self.batch, self.heads, 1, 1), w.view(shape), counts))
+
     def key_counts(self) -> torch.Tensor:
         """Keys per sequence including the current token: packed + tail + 1 (device)."""
         return self.packed_tokens + self.tail_tokens + 1
@@ -621,12 +641,12 @@ def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scalin
     if paired_dense:
         out0, out1, logits = layer.dense_source_attention_pair(
             queries=queries[:2], current_keys=keys[:2], current_values=values[:2], scaling=scaling)
+        idx, valid, mass, w, counts = layer.select_decode_keys(logits, fraction)
     else:
         out0, _ = layer.dense_source_attention(0, query=queries[0], current_key=keys[0], current_value=values[0],
                                                scaling=scaling, return_logits=False)
-        out1, logits = layer.dense_source_attention(1, query=queries[1], current_key=keys[1],
-                                                    current_value=values[1], scaling=scaling, return_logits=True)
-    idx, valid, mass, w, counts = layer.select_decode_keys(logits, fraction)
+        out1, logits, (idx, valid, mass, w, counts) = layer.dense_source_attention_select(
+            1, query=queries[1], current_key=keys[1], current_value=values[1], scaling=scaling, fraction=fraction)
     if fused_source:
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=keys[2], current_value=values[2], indices=idx, valid=valid,

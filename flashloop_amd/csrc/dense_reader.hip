@@ -15,7 +15,8 @@
 //   q . deq_s(K)[t] = sum_c (q_c*scale_{g,c}) * code_{t,c} + sum_c q_c*min_{g,c};
 // V (per-token metadata) likewise:
 //   sum_t p_t*(scale_t*code_t,c + min_t) = sum_t (p_t*scale_t)*code_t,c + sum_t p_t*min_t.
-#include "reader_common.h"
+#include "dense_layout.h"
+#include "internal.h"
 
 #include <mutex>
 #include <vector>
@@ -37,41 +38,6 @@ struct DenseArgs {
   const uint16_t* tail_v;
   int waves;  // persistent waves in the grid
 };
-
-// ---------------------------------------------------------------------------------
-// Global work sequence.  Row bh = b*H + h contributes kTailUnits units for its BF16 tail
-// (+ current token) followed by its G_b prefix groups, G_b = packed_tokens[b] / 64
-// (clamped to the capacity, so a bad length cannot fault).  Wave w owns units
-// [w*chunk, min((w+1)*chunk, U)), chunk = ceil(U / waves): it runs the tails whose first
-// unit it owns and streams the prefix groups it owns.  Counting a tail as kTailUnits
-// groups keeps the waves that also run tails from finishing last.  A wave's partial for
-// row bh goes to slot w + bh: the slots of one row are contiguous and disjoint from every
-// other row's.
-// ---------------------------------------------------------------------------------
-constexpr int kTailUnits = 3;  // measured best among 1..12 at cfg3 (contiguous-range wave partition)
-constexpr int kLenCache = 1024;  // batches whose group counts are cached in LDS
-
-__device__ __forceinline__ int row_groups(const fl_cache_view& v, int b) {
-  return max(min(v.packed_tokens[b], v.token_capacity), 0) / kGroup;
-}
-
-// Group counts per batch: from LDS for the first kLenCache batches (no global load in
-// the streaming loop), from the length array beyond.
-struct RowLens {
-  const int* lds;
-  int n;
-  __device__ __forceinline__ int operator()(const fl_cache_view& v, int b) const {
-    return b < n ? lds[b] : row_groups(v, b);
-  }
-};
-
-__device__ __forceinline__ int64_t total_units(const fl_cache_view& v, const RowLens& rl) {
-  int64_t u = 0;
-  for (int b = 0; b < v.batch; ++b) u += static_cast<int64_t>(v.heads) * (kTailUnits + rl(v, b));
-  return u;
-}
-
-__device__ __forceinline__ int64_t chunk_of(int64_t U, int waves) { return (U + waves - 1) / waves; }
 
 // Position in the work sequence: row (b, h), group gi of gb, row's first unit vs.
 struct Cursor {
@@ -718,41 +684,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
   dense_range<2, true>(a1, mine.l2, rl, w, max(u0, U) - U, max(u1, U) - U);
 }
 
-// Combine row bh's partials: prefix slots [f+bh, l+bh] (see partial_slot) + its tail slot.
-// `pieces` loops were read by one launch (dense_pair_kernel: 2): block p*BH + bh merges
-// row bh of piece p, whose units follow those of the earlier pieces.
+// Combine row bh's partials (dense_merge_row).  `pieces` loops were read by one launch
+// (dense_pair_kernel: 2): block p*BH + bh merges row bh of piece p.
 __global__ __launch_bounds__(kMergeThreads) void dense_merge_kernel(const float* ws0, const float* ws1, int W,
                                                                     fl_cache_view v, float* out0, float* out1,
                                                                     int pieces) {
-  __shared__ int lens[kLenCache];
-  __shared__ MergeLdsBuf S;
-  for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kMergeThreads) lens[i] = row_groups(v, i);
-  __syncthreads();
-  const RowLens rl{lens, min(v.batch, kLenCache)};
-  const int BH = v.batch * v.heads;
-  const int piece = blockIdx.x / BH;
-  const int bh = blockIdx.x - piece * BH;
-  const float* ws = piece == 0 ? ws0 : ws1;
-  float* out = piece == 0 ? out0 : out1;
-  const int b = bh / v.heads, h = bh - (bh / v.heads) * v.heads;
-  int64_t vs = 0, U = 0;
-  for (int bb = 0; bb < v.batch; ++bb) {
-    const int64_t span = static_cast<int64_t>(v.heads) * (kTailUnits + rl(v, bb));
-    if (bb < b) vs += span;
-    U += span;
-  }
-  const int gb = rl(v, b);
-  vs += static_cast<int64_t>(h) * (kTailUnits + gb) + piece * U;
-  int64_t f = 0, l = -1;
-  if (gb > 0) {
-    const int64_t chunk = chunk_of(pieces * U, W);
-    f = (vs + kTailUnits) / chunk;
-    l = (vs + kTailUnits + gb - 1) / chunk;
-  }
-  const MergeParts P{ws + (f + bh) * kPartial, static_cast<int>(l - f + 1),
-                     ws + (static_cast<int64_t>(W) + BH + bh) * kPartial};
-  const float r = merge_softmax(P, S);
-  if (threadIdx.x < kDim) out[static_cast<int64_t>(bh) * kDim + threadIdx.x] = r;
+  __shared__ DenseMergeLds S;
+  dense_merge_row(S, blockIdx.x, ws0, ws1, W, v, out0, out1, pieces);
 }
 
 int cu_count() {
@@ -945,10 +883,11 @@ int32_t dense_checks(const fl_cache_view* view, int32_t loop, const uint16_t* q,
 
 namespace fl {
 namespace {
-// One dense read on a checked workspace: the reader launch and its merge.
+// One dense read on a checked workspace: the reader launch and (with `merge`) its merge;
+// *waves receives the reader's grid size in waves.
 int32_t dense_launch(const fl_cache_view& v, int32_t loop, const uint16_t* q, const uint16_t* k_cur,
                      const uint16_t* v_cur, float scaling, float* out, float* logits, int64_t logits_stride,
-                     float* ws, hipStream_t st) {
+                     float* ws, hipStream_t st, bool merge = true, int* waves = nullptr) {
   DenseArgs a{};
   a.v = v;
   a.q = q;
@@ -979,6 +918,8 @@ int32_t dense_launch(const fl_cache_view& v, int32_t loop, const uint16_t* q, co
   }
   profile_after(st);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(reader)");
+  if (waves) *waves = a.waves;
+  if (!merge) return FL_OK;
   hipLaunchKernelGGL(dense_merge_kernel, dim3(v.batch * v.heads), dim3(kMergeThreads), 0, st,
                      static_cast<const float*>(a.ws), static_cast<const float*>(a.ws), a.waves, v, out, out, 1);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(merge)");
@@ -1029,6 +970,34 @@ extern "C" int32_t fl_decode_attn_dense(const fl_cache_view* view, int32_t loop,
   FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense: workspace too small");
   return dense_launch(*view, loop, q, k_cur, v_cur, scaling, out, logits, logits_stride, static_cast<float*>(workspace),
                       static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t fl_decode_attn_dense_select(const fl_cache_view* view, int32_t loop, const uint16_t* q,
+                                               const uint16_t* k_cur, const uint16_t* v_cur, float scaling,
+                                               float* out, float* logits, int64_t logits_stride, double fraction,
+                                               int32_t capacity, int32_t* indices, uint8_t* valid, float* mass,
+                                               float* weights, int32_t* counts, int32_t* nonfinite, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+  using namespace fl;
+  clear_error();
+  if (const int32_t rc = dense_checks(view, loop, q, k_cur, v_cur, out, logits, logits_stride, workspace); rc != FL_OK)
+    return rc;
+  FL_REQUIRE(logits != nullptr, "fl_decode_attn_dense_select: logits are required");
+  FL_REQUIRE(indices && valid && mass && weights, "fl_decode_attn_dense_select: null selection output");
+  FL_REQUIRE(capacity > 0, "fl_decode_attn_dense_select: bad capacity");
+  FL_REQUIRE(fraction > 0.0 && fraction <= 1.0, "fl_decode_attn_dense_select: fraction must be in (0, 1]");
+  FL_REQUIRE(select_merge_fits(logits_stride, fraction), "fl_decode_attn_dense_select: logits_stride above 35840 "
+             "keys or a selection above 8192 keys (use fl_decode_attn_dense + fl_decode_topk)");
+  FL_REQUIRE(workspace_bytes >= fl_decode_attn_dense_workspace(view), "fl_decode_attn_dense_select: workspace too small");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* ws = static_cast<float*>(workspace);
+  int waves = 0;
+  if (const int32_t rc = dense_launch(*view, loop, q, k_cur, v_cur, scaling, out, logits, logits_stride, ws, st,
+                                      false, &waves);
+      rc != FL_OK)
+    return rc;
+  return launch_select_merge(*view, ws, waves, out, logits, logits_stride, fraction, capacity, indices, valid, mass,
+                             weights, counts, nonfinite, st);
 }
 
 extern "C" size_t fl_decode_attn_dense_noalloc_max_bytes(void) { return fl::kScratchBytes; }

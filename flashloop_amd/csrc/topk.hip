@@ -14,7 +14,8 @@
 // k-th largest key K* and how many keys equal to K* to take, then a final pass walks the
 // row in index order, takes every key > K* and the first `need` keys == K*
 // (ballot/popcount ranks), and writes the selected indices in ascending order.
-#include "fl_common.h"
+#include "dense_layout.h"
+#include "internal.h"
 
 namespace fl {
 namespace {
@@ -382,18 +383,29 @@ __device__ uint32_t prefix_counts(ResShared& sh) {
   return sh.total;
 }
 
-template <int PER>
-__global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(const float* scores, int64_t stride,
-                                                                            const int32_t* n_keys, int rows_per_count,
-                                                                            double fraction, int cap, int32_t* indices,
-                                                                            uint8_t* valid, float* mass, float* weights,
-                                                                            int32_t* counts, int32_t* nonfinite) {
-  __shared__ ResShared sh;
+struct TopkArgs {
+  const float* scores;
+  int64_t stride;
+  double fraction;
+  int cap;
+  int32_t* indices;
+  uint8_t* valid;
+  float* mass;
+  float* weights;
+  int32_t* counts;
+  int32_t* nonfinite;
+};
+
+// Top-k of row r = blockIdx.x (key_count(r) keys) by one 1024-thread workgroup.
+template <int PER, typename KeyCount>
+__device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_count, const float* scores, int64_t stride,
+                                                  double fraction, int cap, int32_t* indices, uint8_t* valid,
+                                                  float* mass, float* weights, int32_t* counts, int32_t* nonfinite) {
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const float* x = scores + static_cast<int64_t>(r) * stride;
-  int n = min(n_keys[r / rows_per_count], static_cast<int>(min<int64_t>(stride, 0x7fffffff)));
+  int n = min(key_count(r), static_cast<int>(min<int64_t>(stride, 0x7fffffff)));
   n = min(n, PER * kTopkThreads);
   int32_t* oi = indices + static_cast<int64_t>(r) * cap;
   uint8_t* ov = valid + static_cast<int64_t>(r) * cap;
@@ -689,6 +701,49 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(cons
   }
 }
 
+template <int PER>
+__global__ __launch_bounds__(kTopkThreads) void decode_topk_resident_kernel(const float* scores, int64_t stride,
+                                                                            const int32_t* n_keys, int rows_per_count,
+                                                                            double fraction, int cap, int32_t* indices,
+                                                                            uint8_t* valid, float* mass, float* weights,
+                                                                            int32_t* counts, int32_t* nonfinite) {
+  __shared__ ResShared sh;
+  topk_resident_row<PER>(
+      sh, [&](int r) { return n_keys[r / rows_per_count]; }, scores, stride, fraction, cap, indices, valid, mass,
+      weights, counts, nonfinite);
+}
+
+// The loop-2 top-k and the merge of the dense reader's rows in one launch: workgroups
+// [0, B*H) select the keys of one row each (a row's key count is its packed prefix + tail +
+// the current token, read from the cache view), workgroups [B*H, 2*B*H) merge one row's
+// partials each.  The two halves are independent (both read only what the reader wrote),
+// and the top-k's one-workgroup-per-row grid leaves half of the CUs free for the merges.
+union SelectMergeLds {
+  ResShared t;
+  reader::DenseMergeLds m;
+};
+
+template <int PER>
+__global__ __launch_bounds__(kTopkThreads) void select_merge_kernel(TopkArgs A, fl_cache_view v, const float* ws, int W,
+                                                                    float* out) {
+  __shared__ SelectMergeLds L;
+  const int rows = v.batch * v.heads;
+  if (static_cast<int>(blockIdx.x) < rows) {
+    // row r's keys: its packed prefix, its tail and the current token (what the reader wrote)
+    const auto key_count = [&](int r) {
+      const int b = r / v.heads;
+      return reader::row_groups(v, b) * kGroup + min(max(v.tail_tokens[b], 0), v.tail_capacity) + 1;
+    };
+    topk_resident_row<PER>(L.t, key_count, A.scores, A.stride, A.fraction, A.cap, A.indices, A.valid, A.mass,
+                           A.weights, A.counts, A.nonfinite);
+    return;
+  }
+  // the merge uses the first kMergeThreads threads; the other waves leave (a workgroup
+  // barrier waits only for waves that have not ended)
+  if (threadIdx.x >= reader::kMergeThreads) return;
+  reader::dense_merge_row(L.m, blockIdx.x - rows, ws, ws, W, v, out, out, 1);
+}
+
 struct EligibleCand {
   const uint8_t* elig;
   int last;  // excluded index (forced), or -1
@@ -771,6 +826,35 @@ __global__ __launch_bounds__(kTopkThreads) void select_tokens_kernel(const float
 }
 
 }  // namespace
+}  // namespace fl
+
+namespace fl {
+// Launch of select_merge_kernel after a dense read of `v` whose partials are at `ws` (W
+// waves): the top-k of the read's logits and the merge of its rows into `out`.
+int32_t launch_select_merge(const fl_cache_view& v, const float* ws, int W, float* out, const float* logits,
+                            int64_t logits_stride, double fraction, int32_t capacity, int32_t* indices,
+                            uint8_t* valid, float* mass, float* weights, int32_t* counts, int32_t* nonfinite,
+                            hipStream_t st) {
+  FL_REQUIRE(select_merge_fits(logits_stride, fraction), "fl_decode_attn_dense_select: logits_stride "
+             "above 35840 keys or a selection above 8192 keys (use fl_decode_attn_dense + fl_decode_topk)");
+  const TopkArgs A{logits, logits_stride, fraction, capacity, indices, valid, mass, weights, counts, nonfinite};
+  const int rows = v.batch * v.heads;
+  const int per = static_cast<int>((logits_stride + kTopkThreads - 1) / kTopkThreads);
+  const dim3 grid(2 * rows), block(kTopkThreads);
+  if (per <= 9)
+    hipLaunchKernelGGL(select_merge_kernel<9>, grid, block, 0, st, A, v, ws, W, out);
+  else if (per <= 18)
+    hipLaunchKernelGGL(select_merge_kernel<18>, grid, block, 0, st, A, v, ws, W, out);
+  else
+    hipLaunchKernelGGL(select_merge_kernel<kPer>, grid, block, 0, st, A, v, ws, W, out);
+  FL_LAUNCH_CHECK("fl_decode_attn_dense_select(select+merge)");
+  return FL_OK;
+}
+
+bool select_merge_fits(int64_t logits_stride, double fraction) {
+  return logits_stride > 0 && logits_stride <= kResKeys &&
+         std::ceil(static_cast<double>(logits_stride) * fraction) <= kSelLds;
+}
 }  // namespace fl
 
 extern "C" int32_t fl_decode_topk(const float* scores, int64_t scores_stride, int32_t rows, const int32_t* n_keys,

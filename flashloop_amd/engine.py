@@ -431,11 +431,14 @@ class FlashLoopEngine:
                 cur_v[li][loop] = v
                 lc = cache.layers[li]
                 if loop < 2 or not sparse:
-                    out, lg = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
-                                                        scaling=a.scaling, return_logits=(loop == 1 and sparse))
+                    if loop == 1 and sparse:  # read, merge and loop-2 selection: two launches
+                        out, lg, (idx, valid, mass, sw, _) = lc.dense_source_attention_select(
+                            loop, query=q, current_key=k, current_value=v, scaling=a.scaling, fraction=fraction)
+                    else:
+                        out, _ = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
+                                                           scaling=a.scaling, return_logits=False)
                     projected = kernels.gemv(out.reshape(bsz, -1), [w["o"]])
                     if loop == 1 and sparse:
-                        idx, valid, mass, sw, _ = lc.select_decode_keys(lg, fraction)
                         sources[li] = _LayerSource(projected, idx, valid, mass, sw, v)
                 else:
                     src = sources[li]
@@ -489,11 +492,14 @@ class FlashLoopEngine:
                 cur_v[li][loop] = v
                 lc = cache.layers[li]
                 if loop < 2 or not sparse:
-                    out, lg = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
-                                                        scaling=a.scaling, return_logits=(loop == 1 and sparse))
+                    if loop == 1 and sparse:
+                        out, lg, (idx, valid, mass, w, _) = lc.dense_source_attention_select(
+                            loop, query=q, current_key=k, current_value=v, scaling=a.scaling, fraction=fraction)
+                    else:
+                        out, _ = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
+                                                           scaling=a.scaling, return_logits=False)
                     projected = a.o_proj(out.to(q.dtype).transpose(1, 2).reshape(bsz, 1, -1))
                     if loop == 1 and sparse:
-                        idx, valid, mass, w, _ = lc.select_decode_keys(lg, fraction)
                         sources[li] = _LayerSource(projected, idx, valid, mass, w, v)
                 else:
                     src = sources[li]

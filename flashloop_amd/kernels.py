@@ -123,6 +123,46 @@ def fused_dense_source_attention(view, loop, query, current_key, current_value, 
     return out, (logits if return_logits else None)
 
 
+SELECT_MAX_STRIDE = 35 * 1024  # logits rows the register-resident top-k holds
+SELECT_MAX_KEYS = 8 * 1024     # selections its LDS list holds
+
+
+def dense_select_fits(logits_capacity: int, fraction: float) -> bool:
+    """Whether ``fused_dense_select`` takes rows of this stride at this fraction."""
+    return 0 < logits_capacity <= SELECT_MAX_STRIDE and math.ceil(logits_capacity * fraction) <= SELECT_MAX_KEYS
+
+
+def fused_dense_select(view, loop, query, current_key, current_value, scaling, fraction, capacity, *,
+                       logits_capacity, device, workspace: Workspace | None = None):
+    """Dense read of loop ``loop`` with logits, then the top-k of those logits and the merge
+    of the read's rows in one launch (``fl_decode_attn_dense_select``): the results of
+    ``fused_dense_source_attention(..., return_logits=True)`` followed by
+    ``decode_topk`` on each row's ``packed + tail + 1`` keys, two launches instead of three
+    (plus the key-count arithmetic).  Returns (out, logits, indices, valid, mass, weights,
+    counts)."""
+    lib = load()
+    rows = view.batch * view.heads
+    q = _vec(query, rows, "query")
+    kc = _vec(current_key, rows, "current_key")
+    vc = _vec(current_value, rows, "current_value")
+    out = torch.empty(rows, HEAD_DIM, dtype=torch.float32, device=device)
+    logits = torch.empty(rows, logits_capacity, dtype=torch.float32, device=device)
+    idx = torch.empty(rows, capacity, dtype=torch.int32, device=device)
+    valid = torch.empty(rows, capacity, dtype=torch.uint8, device=device)
+    mass = torch.empty(rows, dtype=torch.float32, device=device)
+    w = torch.empty(rows, capacity, dtype=torch.float32, device=device)
+    counts = torch.empty(rows, dtype=torch.int32, device=device)
+    ws_bytes = lib.fl_decode_attn_dense_workspace(C.byref(view))
+    ws = (workspace or _WS).get(ws_bytes, device)
+    rc = lib.fl_decode_attn_dense_select(
+        C.byref(view), loop, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), float(scaling), out.data_ptr(),
+        logits.data_ptr(), logits.shape[1], float(fraction), capacity, idx.data_ptr(), valid.data_ptr(),
+        mass.data_ptr(), w.data_ptr(), counts.data_ptr(), None, ws.data_ptr(), ws.numel(), _stream(),
+    )
+    check(rc, "fl_decode_attn_dense_select")
+    return out, logits, idx, valid, mass, w, counts
+
+
 def decode_capacity(keys: int, fraction: float) -> int:
     """Budget and padded capacity (flashloop/engine.py:443-452, 84-109)."""
     k = min(keys, max(1, math.ceil(keys * fraction)))

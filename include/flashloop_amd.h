@@ -224,6 +224,27 @@ int32_t fl_decode_topk(const float* scores, int64_t scores_stride, int32_t rows,
                        float* weights, int32_t* counts, int32_t* nonfinite, void* stream);
 
 /*
+ * J2 + J3 -- the loop-2 dense read and its key selection in two launches instead of
+ * three: fl_decode_attn_dense(view, loop, ..., logits required) followed by
+ * fl_decode_topk on the logits rows with n = packed_tokens[b] + tail_tokens[b] + 1 keys
+ * for the rows of batch b -- the `dense_source_attention(loop=1, return_logits=True)` +
+ * selection sequence of `FlashLoopEngine.decode` (flashloop/engine.py:422-453, 84-109;
+ * flashloop/cache.py:1644-1756).  The reader launch is followed by one launch whose
+ * first B*H workgroups select the keys of one row each while the others merge the
+ * reader's rows (the top-k's one-workgroup-per-row grid leaves them free); results are
+ * bit-identical to the two calls.  Rows must fit the register-resident top-k:
+ * logits_stride <= 35840 and ceil(logits_stride * fraction) <= 8192, otherwise
+ * FL_E_INVALID (use the two calls).  Workspace: fl_decode_attn_dense_workspace() bytes,
+ * as for fl_decode_attn_dense.  No counterpart in the reference as one call.
+ */
+int32_t fl_decode_attn_dense_select(const fl_cache_view* view, int32_t loop,
+                                    const uint16_t* q, const uint16_t* k_cur, const uint16_t* v_cur,
+                                    float scaling, float* out, float* logits, int64_t logits_stride,
+                                    double fraction, int32_t capacity, int32_t* indices, uint8_t* valid,
+                                    float* mass, float* weights, int32_t* counts, int32_t* nonfinite,
+                                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * J2 (sparse) -- weighted sum of selected V rows of loop `loop`.
  *
  * Replaces `pv_cross_loop_cuda` (flashloop/csrc/kivi_outer_gemv_cuda.h:54-67, kernel

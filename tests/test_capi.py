@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 @pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
 def test_argument_errors_are_reported_without_launching():
     lib = _lib.load()
-    assert lib.fl_abi_version() == 2
+    assert lib.fl_abi_version() == 3
     rc = lib.fl_decode_topk(None, 1, 1, None, 1, 0.1, 64, None, None, None, None, None, None, None)
     assert rc == _lib.FL_E_INVALID
     assert b"null" in lib.fl_last_error()

@@ -227,14 +227,16 @@ def test_cfg4_full_model_prefill_and_decode():
     lc = eager.state.cache.layers[0]
     assert lc.quantized_tokens == 8128
     seen = []
-    orig = lc.select_decode_keys
+    orig = lc.dense_source_attention_select
+    check_sel = lc.select_decode_keys
 
-    def spy(logits, fraction, validate=False):
-        res = orig(logits, fraction, validate=True)  # NaN/inf logits would raise here
-        seen.append(res[4])
+    def spy(loop, **kw):
+        res = orig(loop, **kw)
+        check_sel(res[1], kw["fraction"], validate=True)  # NaN/inf logits would raise here
+        seen.append(res[2][4])
         return res
 
-    lc.select_decode_keys = spy
+    lc.dense_source_attention_select = spy
     tok = torch.argmax(outs[0].logits, dim=-1, keepdim=True)
     worst = 1.0
     for step in range(70):

@@ -639,3 +639,36 @@ def test_topk_crowded_boundary_bin_and_very_long_rows():
     sel = OA.decode_topk(lg, 0.1, kpad=cap)
     assert np.array_equal(idx.cpu().numpy(), sel.indices)
     assert np.allclose(mass.cpu().numpy(), sel.mass, rtol=2e-6)
+
+
+@pytest.mark.parametrize("case", ["uniform", "ragged", "many-batches", "full-fraction"])
+def test_dense_select_matches_separate_calls(case):
+    """fl_decode_attn_dense_select (reader launch, then the top-k and the row merges in one
+    launch) against fl_decode_attn_dense + fl_decode_topk: outputs, logits and the whole
+    selection bit for bit, for equal and ragged lengths (key counts read from the cache
+    view), more batches than the length caches, and fraction 1."""
+    print("case: dense select %s" % case, flush=True)
+    frac = 1.0 if case == "full-fraction" else 0.10
+    if case == "ragged":
+        w = decode_workload(5, 3, 0, seed=31, lengths=ragged_lengths(5, 70, 3000, seed=31))
+    elif case == "many-batches":
+        w = decode_workload(1030, 1, 0, seed=32, lengths=ragged_lengths(1030, 65, 260, seed=32))
+    else:
+        w = decode_workload(2, 16, 4000, seed=33)
+    layer = _build(w)
+    q = w.queries[1].to(DEV)
+    kc, vc = (x.to(DEV) for x in w.current(1))
+    out_a, lg_a = layer.dense_source_attention(1, query=q, current_key=kc, current_value=vc, scaling=SCALING,
+                                               return_logits=True)
+    sel_a = layer.select_decode_keys(lg_a, frac)
+    out_b, lg_b, sel_b = layer.dense_source_attention_select(1, query=q, current_key=kc, current_value=vc,
+                                                             scaling=SCALING, fraction=frac)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b), "outputs differ"
+    nk = layer.key_counts().cpu().tolist()
+    la, lb = lg_a.reshape(layer.rows, -1), lg_b.reshape(layer.rows, -1)
+    for r in range(layer.rows):
+        n = nk[r // layer.heads]
+        assert torch.equal(la[r, :n], lb[r, :n]), f"logits row {r}"
+    for name, a, b in zip(("indices", "valid", "mass", "weights", "counts"), sel_a, sel_b):
+        assert torch.equal(a, b), f"{name} differ"
