@@ -100,9 +100,9 @@ constexpr int kNew = 2;   // groups a tile may add to the ring
 
 template <int NS, int LPT>
 struct TileLds {
-  float qs[kRing][NS][kDim];  // q*scale of group g in ring slot g % kRing (odd channels pre-divided by 16)
-  float qm[kRing][NS][LPT];   // q.min per part
-  float qs1[NS][kDim];        // one group for tiles that do not fit the ring
+  uint32_t qs[kRing][NS][kDim / 2];  // fp16 q*scale*2^-E of group g in ring slot g % kRing (dot8h2 pairs)
+  float qm[kRing][NS][LPT];          // q.min per part
+  uint32_t qs1[NS][kDim / 2];        // one group for tiles that do not fit the ring
   float qm1[NS][LPT];
   float qf[kDim];             // q*scaling of the current row
 };
@@ -429,6 +429,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   TileOut<LPT, MODE> o;
   tile_reset<LPT, MODE>(o);
   int cur_bh = -1, nseg = 0;
+  // the row's q*scaling is staged as fp16 factors q*scale*2^-E, with 2^E above max|q*scaling|
+  // so that every factor is at most |scale| (a finite fp16 scale gives a finite factor)
+  float qn = 1.0f, qe = kSub16;  // 2^-E and 2^(24+E)
 
   // ---- stage 4: the arithmetic of a tile
   auto compute = [&](Tile& T) {
@@ -447,8 +450,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       cur_bh = bh;
       if (kSoftmax) {
         wave_sync_lds();
-        L.qf[2 * lane] = bf16lo_to_f32(T.qw) * a.scaling;
-        L.qf[2 * lane + 1] = bf16hi_to_f32(T.qw) * a.scaling;
+        const float f0 = bf16lo_to_f32(T.qw) * a.scaling, f1 = bf16hi_to_f32(T.qw) * a.scaling;
+        L.qf[2 * lane] = f0;
+        L.qf[2 * lane + 1] = f1;
+        const float amax = wave_max(fmaxf(fabsf(f0), fabsf(f1)));
+        int e = 0;
+        if (amax > 0.0f && amax <= 3.0e38f) frexpf(amax, &e);
+        e = min(max(e, -100), 100);
+        qn = ldexpf(1.0f, -e);
+        qe = ldexpf(kSub16, e);
       }
     }
 #ifdef FL_GATHER_NOCOMPUTE
@@ -491,11 +501,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       const float q0 = L.qf[2 * lane], q1 = L.qf[2 * lane + 1];
       // fp16 (scale, min) of one group and stream -> q*scale (this lane's two channels) and
       // q.min (folded over the kCh/2 lanes of one part)
-      auto stage_group = [&](uint2 km, float* qs, float* qm) {
+      auto stage_group = [&](uint2 km, uint32_t* qs, float* qm) {
         const float sc0 = f16_to_f32(km.x & 0xFFFFu), mn0 = f16_to_f32(km.x >> 16);
         const float sc1 = f16_to_f32(km.y & 0xFFFFu), mn1 = f16_to_f32(km.y >> 16);
-        qs[2 * lane] = (q0 * kSub16) * sc0;  // codes read as fp16 subnormals (dot8h)
-        qs[2 * lane + 1] = (q1 * (kSub16 * 0.0625f)) * sc1;  // high nibbles read as 16*code
+        uint16_t* qh = reinterpret_cast<uint16_t*>(qs);
+        const int at = pair_slot(2 * lane);  // channel 2*lane + 1 sits one pair later
+        qh[at] = __builtin_bit_cast(uint16_t, static_cast<_Float16>((q0 * qn) * sc0));
+        qh[at + 2] = __builtin_bit_cast(uint16_t, static_cast<_Float16>((q1 * (qn * 0.0625f)) * sc1));  // read as 16*code
         float m = fmaf(q0, mn0, q1 * mn1);
         m += dpp<kDppXor1>(m);
         m += dpp<kDppXor2>(m);
@@ -504,7 +516,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         if ((lane & (kCh / 2 - 1)) == 0) qm[lane / (kCh / 2)] = m;
       };
       // logit of this lane's slot from the staged q*scale / q.min of its group
-      auto dot_group = [&](const float (*qs)[kDim], const float (*qm)[LPT]) {
+      auto dot_group = [&](const uint32_t (*qs)[kDim / 2], const float (*qm)[LPT]) {
         float d = 0.0f;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -512,16 +524,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           // (an absent row reads row 0's codes, which the select discards); stream 3 is
           // branched over (selecting it too costs the loop-4 kernel registers it spills)
           if (s == 3 && !((has >> s) & 1u)) continue;
-          const float* qq = &qs[s][kCh * part];
+          const uint32_t* qq = &qs[s][kCh / 2 * part];
           float e = 0.0f;
 #pragma unroll
-          for (int k = 0; k < kWords; ++k) {
-            const float4 x = *reinterpret_cast<const float4*>(qq + 8 * k);
-            const float4 y = *reinterpret_cast<const float4*>(qq + 8 * k + 4);
-            const float qw[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-            e = dot8h(T.kw[s][k], qw, e);
-          }
-          const float t = e + qm[s][part];
+          for (int k = 0; k < kWords; ++k) e = dot8h2(T.kw[s][k], *reinterpret_cast<const uint4*>(qq + 4 * k), e);
+          const float t = fmaf(e, qe, qm[s][part]);
           d += (s != 2 || ((has >> s) & 1u)) ? t : 0.0f;
         }
         return d;

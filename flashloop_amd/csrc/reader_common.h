@@ -57,30 +57,15 @@ __device__ __forceinline__ void axpy8(uint32_t w, float we, float wo, float* acc
   acc[7] = fmaf(wo, ubyte3(hi), acc[7]);
 }
 
-// The same two contractions with the codes read as fp16 subnormals: masking a word with
-// 0x000F000F (0x00F000F0) leaves in each 16-bit half one nibble c (16c) below bit 10, the
-// fp16 value c*2^-24 (16c*2^-24), which v_fma_mix_f32 takes as an exact fp32 operand.
-// Two masks per four codes replace four conversions; the factors carry the 2^24 (and the
-// odd channels' 1/16).  q[0..7]: factors of channels 0..7 of the word.
+// Codes read as fp16 subnormals: masking a word with 0x000F000F (0x00F000F0) leaves in
+// each 16-bit half one nibble c (16c) below bit 10, the fp16 value c*2^-24 (16c*2^-24),
+// which v_fma_mix_f32 and v_dot2_f32_f16 take as exact operands.  Two masks per four
+// codes replace four conversions; the factors carry the 2^24 (and the odd channels' 1/16).
 __device__ __forceinline__ float h16lo(uint32_t x) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x & 0xFFFFu)));
 }
 __device__ __forceinline__ float h16hi(uint32_t x) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x >> 16)));
-}
-__device__ __forceinline__ float dot8h(uint32_t w, const float* q, float acc) {
-  const uint32_t x0 = w & 0x000F000Fu, x1 = w & 0x00F000F0u;
-  const uint32_t w8 = w >> 8;
-  const uint32_t x2 = w8 & 0x000F000Fu, x3 = w8 & 0x00F000F0u;
-  acc = fmaf(q[0], h16lo(x0), acc);
-  acc = fmaf(q[4], h16hi(x0), acc);
-  acc = fmaf(q[1], h16lo(x1), acc);
-  acc = fmaf(q[5], h16hi(x1), acc);
-  acc = fmaf(q[2], h16lo(x2), acc);
-  acc = fmaf(q[6], h16hi(x2), acc);
-  acc = fmaf(q[3], h16lo(x3), acc);
-  acc = fmaf(q[7], h16hi(x3), acc);
-  return acc;
 }
 // acc[c] += we*code_c for even channels, wo*(16*code_c) for odd ones (we, wo scaled by 2^24)
 __device__ __forceinline__ void axpy8h(uint32_t w, float we, float wo, float* acc) {
@@ -97,6 +82,23 @@ __device__ __forceinline__ void axpy8h(uint32_t w, float we, float wo, float* ac
   acc[7] = fmaf(wo, h16hi(x3), acc[7]);
 }
 constexpr float kSub16 = 16777216.0f;  // 2^24: fp16 subnormal code c reads as c * 2^-24
+
+// The K contraction of one code word against fp16 factor pairs, two channels per
+// v_dot2_f32_f16: f.x = (f0, f4), f.y = (f1, f5)/16, f.z = (f2, f6), f.w = (f3, f7)/16
+// for channels 0..7 of the word, whose masked codes are fp16 subnormals c*2^-24 (16c*2^-24
+// for the odd ones).  The products are exact in fp32; the result carries 2^-24.
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot8h2(uint32_t w, uint4 f, float acc) {
+  const uint32_t w8 = w >> 8;
+  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w & 0x000F000Fu), __builtin_bit_cast(half2_t, f.x), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w & 0x00F000F0u), __builtin_bit_cast(half2_t, f.y), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w8 & 0x000F000Fu), __builtin_bit_cast(half2_t, f.z), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w8 & 0x00F000F0u), __builtin_bit_cast(half2_t, f.w), acc, false);
+  return acc;
+}
+// Position (in fp16 units) of channel c's factor in the pair layout dot8h2 reads: word
+// c/8 holds 8 factors, pair (c%8)%4, half (c%8)/4.
+__device__ __forceinline__ int pair_slot(int c) { return (c >> 3) * 8 + (c & 3) * 2 + ((c >> 2) & 1); }
 
 struct QuadState {
   float m, l, mu;
