@@ -766,9 +766,15 @@ int gather_occupancy() {
 
 constexpr int kGatherMaxResident = 4;  // workgroups per CU any reader instantiation holds
 
-// Persistent grid: every resident workgroup slot, fewer when the selection is small.
+#ifndef FL_GATHER_LPT
+#define FL_GATHER_LPT 8
+#endif
+constexpr int kLpt = FL_GATHER_LPT;  // lanes per selected slot
+
+// Persistent grid: one wave per tile up to every resident workgroup slot (a small
+// selection, e.g. batch one, gets one tile per wave: its waves are latency chains).
 int gather_blocks(int rows, int capacity, int occ) {
-  const int64_t tiles = static_cast<int64_t>(rows) * (capacity / 16);  // upper bound over tile sizes
+  const int64_t tiles = static_cast<int64_t>(rows) * (capacity / Lay<kLpt>::kTok);
   const int64_t want = (tiles + kWaves - 1) / kWaves;
   const int64_t slots = static_cast<int64_t>(gather_cu_count()) * std::min(std::max(occ, 1), kGatherMaxResident);
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(slots, want)));
@@ -778,11 +784,6 @@ size_t gather_workspace(int rows, int capacity) {
   const int64_t waves = static_cast<int64_t>(gather_blocks(rows, capacity, kGatherMaxResident)) * kWaves;
   return static_cast<size_t>(2 * (waves + rows)) * kPartial * sizeof(float);
 }
-
-#ifndef FL_GATHER_LPT
-#define FL_GATHER_LPT 8
-#endif
-constexpr int kLpt = FL_GATHER_LPT;  // lanes per selected slot
 
 template <int NS, int MODE>
 void launch_ns(GatherArgs& a, int rows, hipStream_t st) {
