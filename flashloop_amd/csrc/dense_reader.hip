@@ -50,7 +50,7 @@ __device__ __forceinline__ Cursor locate(const fl_cache_view& v, const RowLens& 
   Cursor c{0, 0, 0, 0, 0};
   int64_t base = 0;
   for (int b = 0; b < v.batch; ++b) {
-    const int gb = rl(v, b);
+    const int gb = __builtin_amdgcn_readfirstlane(rl(v, b));  // (wave-uniform)
     const int64_t span = kTailUnits + gb;
     const int64_t all = static_cast<int64_t>(v.heads) * span;
     if (u < base + all) {
@@ -75,7 +75,7 @@ __device__ __forceinline__ void next_row(Cursor& c, const fl_cache_view& v, cons
     c.h = 0;
     ++c.b;
   }
-  c.gb = c.b < v.batch ? rl(v, c.b) : 0;
+  c.gb = c.b < v.batch ? __builtin_amdgcn_readfirstlane(rl(v, c.b)) : 0;  // (wave-uniform)
 }
 
 // Move to the next prefix group (skipping rows without groups); stops past the end.
@@ -646,7 +646,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
   __shared__ ReaderLds<NS, LOGITS> L;
   __shared__ int lens[kLenCache];
   const fl_cache_view& v = a.v;
-  const int w = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  // wave-uniform: the work cursor and every length lookup stay in scalar registers
+  const int w = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   for (int i = threadIdx.x; i < min(v.batch, kLenCache); i += kThreads) lens[i] = row_groups(v, i);
   __syncthreads();
   const RowLens rl{lens, min(v.batch, kLenCache)};
