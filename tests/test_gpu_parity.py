@@ -314,6 +314,21 @@ def test_decode_step_many_batches():
     _step_vs_oracle(w, layer)
 
 
+def test_decode_step_query_and_key_ranges():
+    """The sparse readers stage q*scale as fp16 factors normalised by the row's largest
+    |q*scaling|: heads whose late-loop queries are 1e-3 .. 4 times the unit draw stay at
+    the oracle bar (an unnormalised factor of a 1e-3 query falls into fp16's subnormal
+    range).  Sharper rows (16x) leave the bar with fp32 factors too: the oracle's bf16
+    residual chain, not the factors, sets that error."""
+    print("case: decode step query/key ranges B2 H4 T700", flush=True)
+    w = decode_workload(2, 4, 700, seed=12)
+    f = torch.tensor([1e-3, 0.05, 1.0, 4.0]).view(1, 4, 1, 1)
+    for r in (2, 3):
+        w.queries[r] = (w.queries[r].float() * f).to(torch.bfloat16)
+    layer = _build(w)
+    _step_vs_oracle(w, layer)
+
+
 def test_decode_step_full_fraction_equals_dense():
     """fraction 1 selects every key: loop-2 output + delta == dense loop-3/4 output."""
     print("case: full fraction", flush=True)
