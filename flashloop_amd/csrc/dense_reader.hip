@@ -45,12 +45,20 @@ struct Cursor {
   int64_t vs;
 };
 
+// Group count of batch b (wave-uniform), kept in a scalar register: from the LDS cache,
+// else from the length array (batches past the cache).
+__device__ __forceinline__ int row_len(const fl_cache_view& v, const RowLens& rl, int b) {
+  b = __builtin_amdgcn_readfirstlane(b);
+  if (b < rl.n) return __builtin_amdgcn_readfirstlane(rl.lds[b]);
+  return max(min(v.packed_tokens[b], v.token_capacity), 0) / kGroup;
+}
+
 // Row containing unit u; gi = u's offset within the row's units.
 __device__ __forceinline__ Cursor locate(const fl_cache_view& v, const RowLens& rl, int64_t u) {
   Cursor c{0, 0, 0, 0, 0};
   int64_t base = 0;
   for (int b = 0; b < v.batch; ++b) {
-    const int gb = __builtin_amdgcn_readfirstlane(rl(v, b));  // (wave-uniform)
+    const int gb = row_len(v, rl, b);
     const int64_t span = kTailUnits + gb;
     const int64_t all = static_cast<int64_t>(v.heads) * span;
     if (u < base + all) {
@@ -75,7 +83,7 @@ __device__ __forceinline__ void next_row(Cursor& c, const fl_cache_view& v, cons
     c.h = 0;
     ++c.b;
   }
-  c.gb = c.b < v.batch ? __builtin_amdgcn_readfirstlane(rl(v, c.b)) : 0;  // (wave-uniform)
+  c.gb = c.b < v.batch ? row_len(v, rl, c.b) : 0;
 }
 
 // Move to the next prefix group (skipping rows without groups); stops past the end.
@@ -105,6 +113,10 @@ __host__ __device__ __forceinline__ int64_t partial_slot(int w, int bh) { return
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
+// 16-byte code chunks as a native vector: copies of HIP's uint4 (a struct) became memcpys
+// that SROA left in a per-thread array -- placed in LDS by the compiler, with a store of
+// the first loaded chunk that made each wave wait for its first group's loads.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v2i lds_v2i;
 
 constexpr float kFixScale = 127.0f * 16777216.0f;  // 127 * 2^24
@@ -139,7 +151,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Wave-private LDS of the prefix path.
 template <int NS>
 struct PrefixLds {
-  uint4 vt[NS][256];          // V codes of the group: entry (i*64 + lane) = row 16i+(lane&15), quarter lane>>4
+  u32x4 vt[NS][256];          // V codes of the group: entry (i*64 + lane) = row 16i+(lane&15), quarter lane>>4
   uint32_t y[NS][4][2][4][4];  // K-side digits [stream][digit][parity][quarter][4 words of 4 channels]
   uint32_t z[NS][2][4][16];    // V-side digits [stream][half][digit][16 words of 4 tokens]
 };
@@ -151,9 +163,9 @@ struct PrefixLds {
 template <int NS>
 struct GroupSet {
   uint2 km[NS];  // fp16 (scale, min) of channels 2*lane, 2*lane+1
-  uint4 kw[4][NS];
+  u32x4 kw[4][NS];
   uint2 vm[NS];  // fp16 (scale, min) of both 64-channel halves of token `lane`
-  uint4 vw[4][NS];
+  u32x4 vw[4][NS];
   uint32_t qw;   // bf16 q of channels 2*lane, 2*lane+1
   uint32_t has;  // stream s>=2: bit 5*(s-2)+i row present for tile i, bit 5*(s-2)+4 own token
   int bh, gi;
@@ -165,24 +177,17 @@ __device__ __forceinline__ void load_group(GroupSet<NS>& gs, const DenseArgs& a,
   const int lane = threadIdx.x & 63, n = lane & 15, quarter = lane >> 4;
   const int bh = c.b * v.heads + c.h, gi = c.gi;
   const int gcap = v.token_capacity / kGroup;
-  int rows[NS][5];
+  // Row of token t in stream s (streams 2/3 through the rank map; absent rows read row 0
+  // and are masked by `has`), computed where it is used.
   uint32_t has = 0;
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-#pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int t = gi * kGroup + (i < 4 ? 16 * i + n : lane);
-      int r = t;
-      if (s >= 2) {
-        r = v.rank[s - 2][static_cast<int64_t>(c.b) * v.token_capacity + t];
-        const bool ok = r >= 0 && r < v.row_capacity[s];
-        if (ok) has |= 1u << (5 * (s - 2) + i);
-        else r = 0;
-      }
-      rows[s][i] = r;
-    }
-  }
-  gs.has = has;
+  auto row_of = [&](int s, int i) {
+    const int t = gi * kGroup + (i < 4 ? 16 * i + n : lane);
+    if (s < 2) return t;
+    const int r = v.rank[s - 2][static_cast<int64_t>(c.b) * v.token_capacity + t];
+    const bool ok = r >= 0 && r < v.row_capacity[s];
+    if (ok) has |= 1u << (5 * (s - 2) + i);
+    return ok ? r : 0;
+  };
   gs.bh = bh;
   gs.gi = gi;
   gs.qw = *reinterpret_cast<const uint32_t*>(a.q + static_cast<int64_t>(bh) * kDim + 2 * lane);
@@ -195,14 +200,15 @@ __device__ __forceinline__ void load_group(GroupSet<NS>& gs, const DenseArgs& a,
   for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint8_t* line = v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][i]) * kCodeStride;
-      gs.kw[i][s] = *reinterpret_cast<const uint4*>(line + 16 * quarter);
-      gs.vw[i][s] = *reinterpret_cast<const uint4*>(v.value_codes[s] - v.key_codes[s] + line + 16 * quarter);
+      const uint8_t* line = v.key_codes[s] + (static_cast<int64_t>(bh) * v.row_capacity[s] + row_of(s, i)) * kCodeStride;
+      gs.kw[i][s] = *reinterpret_cast<const u32x4*>(line + 16 * quarter);
+      gs.vw[i][s] = *reinterpret_cast<const u32x4*>(v.value_codes[s] - v.key_codes[s] + line + 16 * quarter);
     }
 #pragma unroll
   for (int s = 0; s < NS; ++s)
     gs.vm[s] = *reinterpret_cast<const uint2*>(v.value_meta_half[s] +
-                                               (static_cast<int64_t>(bh) * v.row_capacity[s] + rows[s][4]) * 4);
+                                               (static_cast<int64_t>(bh) * v.row_capacity[s] + row_of(s, 4)) * 4);
+  gs.has = has;
 }
 
 // Wave-level online-softmax state of the prefix path.  m is wave-uniform; l, mu0/mu1
@@ -213,11 +219,11 @@ struct WaveState {
   float acc[8];
 };
 
-__device__ __forceinline__ v4i nib_lo(uint4 w) {
+__device__ __forceinline__ v4i nib_lo(u32x4 w) {
   return v4i{static_cast<int>(w.x & 0x0F0F0F0Fu), static_cast<int>(w.y & 0x0F0F0F0Fu),
              static_cast<int>(w.z & 0x0F0F0F0Fu), static_cast<int>(w.w & 0x0F0F0F0Fu)};
 }
-__device__ __forceinline__ v4i nib_hi(uint4 w) {
+__device__ __forceinline__ v4i nib_hi(u32x4 w) {
   return v4i{static_cast<int>((w.x >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.y >> 4) & 0x0F0F0F0Fu),
              static_cast<int>((w.z >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.w >> 4) & 0x0F0F0F0Fu)};
 }
@@ -246,8 +252,13 @@ __device__ __forceinline__ void compute_group(const GroupSet<NS>& gs, WaveState&
     c[s] = fmaf(q0, km0, q1 * km1);
   }
   // streams 0/1 are present for every token: one reduction of their sum
-  c[0] = wave_sum(NS > 1 ? c[0] + c[1] : c[0]);
-  if (NS > 1) c[1] = 0.0f;
+  // (if constexpr: no index past the one-stream arrays)
+  if constexpr (NS > 1) {
+    c[0] = wave_sum(c[0] + c[1]);
+    c[1] = 0.0f;
+  } else {
+    c[0] = wave_sum(c[0]);
+  }
 #pragma unroll
   for (int s = 2; s < NS; ++s) c[s] = wave_sum(c[s]);
   ymax = wave_max(ymax);
@@ -273,11 +284,11 @@ __device__ __forceinline__ void compute_group(const GroupSet<NS>& gs, WaveState&
     float cadd = 0.0f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      uint4 w = gs.kw[i][s];
+      u32x4 w = gs.kw[i][s];
       bool ok = true;
       if (s >= 2) {
         ok = (gs.has >> (5 * (s - 2) + i)) & 1u;
-        if (!ok) w = make_uint4(0, 0, 0, 0);
+        if (!ok) w = u32x4{0u, 0u, 0u, 0u};
       }
       d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ae[s], nib_lo(w), d, 0, 0, 0);
       d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ao[s], nib_hi(w), d, 0, 0, 0);
@@ -392,7 +403,7 @@ __device__ void wave_tail(const DenseArgs& a, int bh, float (*comb)[kDim]) {
   // would wait for it); every load is unconditional: rows past the end read the current
   // token's row and are masked.
   struct Rows {
-    uint4 k[4], v[4];
+    u32x4 k[4], v[4];
   };
   auto fetch = [&](Rows& r, int base) __attribute__((always_inline)) {
     const int vt = base + row;
@@ -400,8 +411,8 @@ __device__ void wave_tail(const DenseArgs& a, int bh, float (*comb)[kDim]) {
     const uint16_t* vr = (vt < tl) ? tv + static_cast<int64_t>(vt) * kDim : cv;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      r.k[k] = *reinterpret_cast<const uint4*>(kr + 32 * quarter + 8 * k);
-      r.v[k] = *reinterpret_cast<const uint4*>(vr + 32 * quarter + 8 * k);
+      r.k[k] = *reinterpret_cast<const u32x4*>(kr + 32 * quarter + 8 * k);
+      r.v[k] = *reinterpret_cast<const u32x4*>(vr + 32 * quarter + 8 * k);
     }
   };
   auto step = [&](const Rows& r, int base) __attribute__((always_inline)) {
@@ -410,7 +421,7 @@ __device__ void wave_tail(const DenseArgs& a, int bh, float (*comb)[kDim]) {
     float d = 0.0f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint4 w = r.k[k];
+      const u32x4 w = r.k[k];
       d = fmaf(qr[8 * k + 0], bf16lo_to_f32(w.x), d);
       d = fmaf(qr[8 * k + 1], bf16hi_to_f32(w.x), d);
       d = fmaf(qr[8 * k + 2], bf16lo_to_f32(w.y), d);
@@ -436,15 +447,25 @@ __device__ void wave_tail(const DenseArgs& a, int bh, float (*comb)[kDim]) {
       }
     }
   };
+  // Peeled like the prefix loop: the steady-state body has no exit between a set's fetch
+  // and its use, so the compiler's waits count only the younger set's loads (an exit
+  // between them made it wait for every load, one full round trip per 16 rows).
+  const int steps = (n + 15) / 16;
   Rows ra, rb;
   fetch(ra, 0);
-  for (int base = 0;; base += 32) {
-    fetch(rb, base + 16);
-    step(ra, base);
-    if (base + 16 >= n) break;
-    fetch(ra, base + 32);
-    step(rb, base + 16);
-    if (base + 32 >= n) break;
+  int s = 0;
+  for (; s + 2 < steps; s += 2) {
+    fetch(rb, 16 * s + 16);
+    step(ra, 16 * s);
+    fetch(ra, 16 * s + 32);
+    step(rb, 16 * s + 16);
+  }
+  if (steps - s == 2) {
+    fetch(rb, 16 * s + 16);
+    step(ra, 16 * s);
+    step(rb, 16 * s + 16);
+  } else {
+    step(ra, 16 * s);
   }
   const float M = wave_max(st.m);  // finite: the current token is always present
   const float f = st.m == -INFINITY ? 0.0f : fast_exp2((st.m - M) * kLog2e);
@@ -586,7 +607,7 @@ __device__ __forceinline__ void dense_range(const DenseArgs& a, WaveBlock<NS, LO
     stage_partial(st, pbuf[nseg - 1]);
     if ((threadIdx.x & 63) == 0) seg[nseg - 1] = SegMeta{cur_bh, cur_gi0, cur_first, cur_count};
   };
-  auto run = [&](const GroupSet<NS>& gs) {
+  auto run = [&](const GroupSet<NS>& gs) __attribute__((always_inline)) {
     if (gs.bh != cur_bh) {
       if (nseg > 0) close_seg();
       if (nseg == kStageSegs || (LOGITS && used == kStageGroups)) {  // rare: stage full

@@ -105,17 +105,17 @@ struct QuadState {
   float acc[32];
 };
 
+// Branch-free (selects, no early exit): a divergent exit here joins the caller's control
+// flow, and at that join the compiler waits for every load in flight, including the next
+// rows already requested.
 __device__ __forceinline__ void online_update(QuadState& st, const float* lg, float* p, int n) {
   float mloc = st.m;
   for (int i = 0; i < n; ++i) mloc = fmaxf(mloc, lg[i]);
-  if (mloc == -INFINITY) {  // nothing valid yet
-    for (int i = 0; i < n; ++i) p[i] = 0.0f;
-    return;
-  }
-  const float alpha = fast_exp2((st.m - mloc) * kLog2e);
+  const bool none = mloc == -INFINITY;  // nothing valid yet: state unchanged, p = 0
+  const float alpha = none ? 1.0f : fast_exp2((st.m - mloc) * kLog2e);
   float ps = 0.0f;
   for (int i = 0; i < n; ++i) {
-    p[i] = fast_exp2((lg[i] - mloc) * kLog2e);
+    p[i] = none ? 0.0f : fast_exp2((lg[i] - mloc) * kLog2e);
     ps += p[i];
   }
   st.l = st.l * alpha + ps;
