@@ -57,6 +57,9 @@ class CrossLoopKVLayer:
             raise ValueError("token_capacity must be a multiple of 64")
         if g.tail_capacity < self.residual_length + GROUP:
             raise ValueError("tail_capacity must hold 128 rows (residual + one group)")
+        if min(g.row_capacity) < 1:
+            # the readers read row 0 of a stream in place of an absent row (then mask it)
+            raise ValueError("every stream needs a row capacity of at least 1")
         self.geometry = g
         self.device = torch.device(device)
         rows = g.batch * g.heads
@@ -202,7 +205,7 @@ class CrossLoopKVLayer:
             ranks.append(r)
             late_counts.append([int(x) for x in act.sum(dim=1).tolist()])
         growth = cap - min(tp)  # every future decode token is active in every loop
-        row_cap = (cap, cap, max(late_counts[0]) + growth, max(late_counts[1]) + growth)
+        row_cap = (cap, cap, max(max(late_counts[0]) + growth, 1), max(max(late_counts[1]) + growth, 1))
         layer = cls(LayerGeometry(b, h, cap, 2 * GROUP, row_cap), dev)
         for s in range(2):
             layer.rank[s][:, : min(t, cap)] = ranks[s][:, : min(t, cap)]

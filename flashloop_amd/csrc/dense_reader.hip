@@ -893,6 +893,8 @@ int32_t dense_checks(const fl_cache_view* view, int32_t loop, const uint16_t* q,
   for (int s = 0; s <= loop && v.max_packed_tokens > 0; ++s) {
     FL_REQUIRE(v.key_codes[s] && v.key_meta_half[s] && v.value_codes[s] && v.value_meta_half[s],
                "fl_decode_attn_dense: null stream pointer");
+    // an absent row of streams 2/3 reads row 0 (masked)
+    FL_REQUIRE(v.row_capacity[s] > 0, "fl_decode_attn_dense: stream without rows");
     if (s >= 2) FL_REQUIRE(v.rank[s - 2] != nullptr, "fl_decode_attn_dense: null rank map");
   }
   FL_REQUIRE(logits == nullptr || logits_stride >= static_cast<int64_t>(v.max_packed_tokens) + v.max_tail_tokens + 1,

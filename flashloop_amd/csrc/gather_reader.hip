@@ -52,6 +52,14 @@ constexpr int kLenCacheG = 512;  // batches whose lengths a reader caches in LDS
 
 __host__ __device__ __forceinline__ int64_t gather_slot(int w, int bh) { return static_cast<int64_t>(w) + bh; }
 
+// A wave-uniform 64-bit value computed on the vector unit (e.g. a division) moved to
+// scalar registers, so the values derived from it stay scalar too.
+__device__ __forceinline__ int64_t uniform64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(x) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ void axpy_bf16_words(uint4 w, float p, float* acc) {
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -228,7 +236,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int rows = v.batch * v.heads;
   const int tpr = a.cap / Y::kTok;  // tiles per row
   const int64_t total = static_cast<int64_t>(rows) * tpr;
-  const int64_t chunk = (total + a.waves - 1) / a.waves;
+  const int64_t chunk = uniform64((total + a.waves - 1) / a.waves);
   const int64_t t0 = static_cast<int64_t>(w) * chunk;
   const int64_t t1 = min(t0 + chunk, total);
   const int gcap = v.token_capacity / kGroup;
@@ -270,9 +278,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   auto pos_at = [&](int64_t tile) {
     Pos p;
     p.i = tile;
-    p.bh = static_cast<int>(tile / tpr);
-    p.k = static_cast<int>(tile - static_cast<int64_t>(p.bh) * tpr);
-    p.b = p.bh / v.heads;
+    p.bh = __builtin_amdgcn_readfirstlane(static_cast<int>(tile / tpr));
+    p.k = __builtin_amdgcn_readfirstlane(static_cast<int>(tile - static_cast<int64_t>(p.bh) * tpr));
+    p.b = __builtin_amdgcn_readfirstlane(p.bh / v.heads);
     p.h = p.bh - p.b * v.heads;
     return p;
   };
@@ -373,7 +381,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       (void)base;
 #else
       if (kSoftmax) load_words<LPT>(T.kw[s], v.key_codes[s] + base + off);
-      load_words<LPT>(T.vw[s], v.value_codes[s] + base + off);
+      load_words<LPT>(T.vw[s], v.key_codes[s] + base + off + kCodeStride / 2);  // V row: second half of the line
 #endif
     }
     // V metadata of every stream from the token's 64-byte record (this lane's half: 32 bytes)
@@ -722,11 +730,16 @@ int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t
   FL_REQUIRE(v.batch > 0 && v.heads > 0 && v.token_capacity % kGroup == 0, std::string(who) + ": bad view geometry");
   FL_REQUIRE(v.packed_tokens && v.tail_tokens, std::string(who) + ": null length arrays");
   FL_REQUIRE(v.tail_key[loop] && v.tail_value[loop], std::string(who) + ": null tail for this loop");
-  for (int s = 0; s <= loop && v.max_packed_tokens > 0; ++s) {
-    FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s] && v.value_meta_token &&
-                   v.key_meta_half[s],
+  // the readers load row 0 of every stream (and token 0's records) in place of a slot that
+  // is absent there, so these must exist even when no prefix is packed yet
+  FL_REQUIRE(v.token_capacity > 0 && v.value_meta_token, std::string(who) + ": no token records");
+  for (int s = 0; s <= loop; ++s) {
+    FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s] && v.key_meta_half[s],
                std::string(who) + ": null stream pointer");
+    FL_REQUIRE(v.row_capacity[s] > 0, std::string(who) + ": stream without rows");
     if (s >= 2) FL_REQUIRE(v.rank[s - 2] != nullptr, std::string(who) + ": null rank map");
+    FL_REQUIRE(v.value_codes[s] == v.key_codes[s] + kCodeStride / 2,
+               std::string(who) + ": value_codes must be the second half of key_codes' lines");
   }
   FL_REQUIRE(workspace_bytes >= need, std::string(who) + ": workspace too small");
   FL_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, std::string(who) + ": workspace must be 16-byte aligned");

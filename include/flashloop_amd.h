@@ -81,7 +81,7 @@ typedef struct fl_cache_view {
   int32_t heads;
   int32_t token_capacity;  /* multiple of 64 */
   int32_t tail_capacity;
-  int32_t row_capacity[4]; /* row_capacity[0] == row_capacity[1] == token_capacity */
+  int32_t row_capacity[4]; /* row_capacity[0] == row_capacity[1] == token_capacity; all >= 1 */
   uint8_t* key_codes[4];
   float* key_meta[4];
   uint8_t* value_codes[4];
@@ -254,7 +254,9 @@ int32_t fl_decode_attn_dense_select(const fl_cache_view* view, int32_t loop,
  * where index packed_tokens[b]+tail_tokens[b] is the current token (v_cur).
  * indices/valid/weights: [B*H, capacity].  out f32 [B*H, 128].
  * workspace: fl_decode_selected_workspace() bytes, with the same contract as
- * fl_decode_attn_dense.
+ * fl_decode_attn_dense.  The sparse readers (this call and the two below) address V
+ * codes through the K line (the view's value_codes[s] must be key_codes[s] + 64, as
+ * laid out above; FL_E_INVALID otherwise).
  */
 size_t fl_decode_selected_workspace(const fl_cache_view* view, int32_t capacity);
 int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop, const int32_t* indices,

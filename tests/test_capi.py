@@ -78,3 +78,62 @@ def test_struct_layout_matches_header(tmp_path):
     got = [int(x) for x in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     want = [getattr(_lib.FlCacheView, f).offset for f in fields] + [C.sizeof(_lib.FlCacheView)]
     assert got == want
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
+def test_sparse_readers_require_value_codes_in_the_key_lines():
+    """The sparse readers load a token's V codes from the second half of its K line, so a
+    view whose value_codes[s] is not key_codes[s] + 64 is refused before any launch."""
+    lib = _lib.load()
+    v = _lib.FlCacheView()
+    v.batch, v.heads, v.token_capacity, v.tail_capacity = 1, 1, 64, 64
+    v.row_capacity[:] = [64, 64, 64, 64]
+    v.max_packed_tokens = 64
+    v.packed_tokens, v.tail_tokens, v.value_meta_token = 0x1000, 0x1100, 0x1200
+    v.tail_key[0], v.tail_value[0] = 0x1300, 0x1400
+    v.key_codes[0], v.key_meta[0], v.value_meta[0], v.key_meta_half[0] = 0x10000, 0x2000, 0x3000, 0x4000
+
+    def call(value_codes):
+        v.value_codes[0] = value_codes
+        return lib.fl_decode_selected_pv(C.byref(v), 0, 0x5000, 0x6000, 0x7000, 16, 0x8000, 0x9000, 0x100000, 0,
+                                         None)
+
+    assert call(0x20000) == _lib.FL_E_INVALID and b"second half" in lib.fl_last_error()
+    # the laid-out view passes this check and stops at the next one (the workspace size)
+    assert call(0x10000 + 64) == _lib.FL_E_INVALID and b"workspace" in lib.fl_last_error()
+    # absent slots read row 0 of each stream and token 0's record, also with nothing packed
+    # yet: a stream without rows or a missing pointer is refused, never dereferenced
+    v.max_packed_tokens = 0
+    v.row_capacity[0] = 0
+    assert call(0x10000 + 64) == _lib.FL_E_INVALID and b"without rows" in lib.fl_last_error()
+    v.row_capacity[0] = 64
+    v.key_meta_half[0] = 0
+    assert call(0x10000 + 64) == _lib.FL_E_INVALID and b"null stream" in lib.fl_last_error()
+    v.key_meta_half[0] = 0x4000
+    v.value_meta_token = 0
+    assert call(0x10000 + 64) == _lib.FL_E_INVALID and b"token records" in lib.fl_last_error()
+
+
+@pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
+def test_dense_reader_refuses_streams_without_rows():
+    lib = _lib.load()
+    v = _lib.FlCacheView()
+    v.batch, v.heads, v.token_capacity, v.tail_capacity = 1, 1, 64, 128
+    v.row_capacity[:] = [64, 64, 0, 0]
+    v.max_packed_tokens = 64
+    v.packed_tokens, v.tail_tokens = 0x1000, 0x1100
+    v.tail_key[2], v.tail_value[2] = 0x1300, 0x1400
+    for s in range(4):
+        v.key_codes[s], v.value_codes[s] = 0x10000 * (s + 1), 0x10000 * (s + 1) + 64
+        v.key_meta_half[s], v.value_meta_half[s] = 0x2000 + 0x100 * s, 0x3000 + 0x100 * s
+    v.rank[0], v.rank[1] = 0x5000, 0x6000
+    rc = lib.fl_decode_attn_dense(C.byref(v), 2, 0x7000, 0x7100, 0x7200, 1.0, 0x8000, None, 0, 0x100000, 1 << 20,
+                                  None)
+    assert rc == _lib.FL_E_INVALID and b"without rows" in lib.fl_last_error()
+
+
+def test_layer_geometry_needs_a_row_in_every_stream():
+    from flashloop_amd.cache import CrossLoopKVLayer, LayerGeometry
+
+    with pytest.raises(ValueError, match="row capacity"):
+        CrossLoopKVLayer(LayerGeometry(1, 1, 64, 128, (64, 64, 0, 1)), "cpu")

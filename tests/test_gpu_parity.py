@@ -295,6 +295,19 @@ def test_decode_step_masked_late_loops():
     _step_vs_oracle(w, layer, m3, m4)
 
 
+def test_decode_step_late_loops_without_prefix_rows():
+    """No prefix row is recomputed in loops 3/4 and the capacity leaves no room to grow:
+    streams 2/3 hold a single unused row, which the readers read (and mask) in place of
+    every absent row."""
+    print("case: decode step empty late streams B2 H2 T640", flush=True)
+    w = decode_workload(2, 2, 640, seed=13)
+    m3 = np.zeros((2, 640), dtype=bool)
+    layer = _build(w, m3, m3.copy())
+    assert layer.geometry.row_capacity[2:] == (1, 1)
+    assert layer.late_rows_host == [[0, 0], [0, 0]]
+    _step_vs_oracle(w, layer, m3, m3.copy())
+
+
 def test_decode_step_ragged_batch():
     print("case: decode step ragged B3 H2", flush=True)
     lengths = ragged_lengths(3, 100, 900, seed=2)
