@@ -433,7 +433,7 @@ __device__ void wave_tail(const DenseArgs& a, int bh, float (*comb)[kDim]) {
     }
     d = quad_sum(d);
     float lg = valid ? d : -INFINITY;
-    if (LOGITS && quarter == 0 && valid) lrow[Tp + vt] = lg;
+    if (LOGITS && quarter == 0 && valid && Tp + vt < a.logits_stride) lrow[Tp + vt] = lg;
     float p;
     online_update(st, &lg, &p, 1);
     p = valid ? p : 0.0f;
@@ -522,7 +522,10 @@ __device__ __forceinline__ void stage_flush(const DenseArgs& a, const SegMeta* s
     if (LOGITS) {
       float* dst = a.logits + static_cast<int64_t>(m.bh) * a.logits_stride + static_cast<int64_t>(m.gi0) * kGroup;
       const float* src = lgbuf + m.first * kGroup;
-      for (int e = lane; e < m.count * kGroup; e += kWave) dst[e] = src[e];
+      // a row never writes past its stride (device lengths above the host maxima)
+      const int64_t room = a.logits_stride - static_cast<int64_t>(m.gi0) * kGroup;
+      const int cnt = static_cast<int>(min(static_cast<int64_t>(m.count * kGroup), max(room, int64_t{0})));
+      for (int e = lane; e < cnt; e += kWave) dst[e] = src[e];
     }
     if (!(last_open && k == n - 1)) {
       float* part = a.ws + partial_slot(w, m.bh) * kPartial;

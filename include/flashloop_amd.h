@@ -140,7 +140,8 @@ int32_t fl_pack_kv_groups(const fl_cache_view* view, int32_t loops,
  * packed prefix (streams 0..loop, streams 2/3 through the rank maps), then loop
  * `loop`'s tail, then the current token.  q, k_cur, v_cur: bf16 [B*H, 128].
  * out: f32 [B*H, 128].  logits (optional): f32, row bh at `logits + bh*logits_stride`,
- * holding scaling*q.k for the packed_tokens[b] + tail_tokens[b] + 1 keys.
+ * holding scaling*q.k for the packed_tokens[b] + tail_tokens[b] + 1 keys (never written
+ * past logits_stride, should the device lengths exceed the view's host maxima).
  * `loop` in 0..3 (the reference kernel supports 0..1; 2..3 serve
  * enable_sparse_decode=False, flashloop/engine.py:422).
  * workspace: fl_decode_attn_dense_workspace() bytes (16-byte aligned, any content) for the

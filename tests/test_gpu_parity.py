@@ -166,6 +166,42 @@ def test_dense_reader_all_loops(masked):
         assert_close(got_lg[:, : want_lg.shape[1]], want_lg, max_abs=2e-2, mean_abs=5e-3, what=f"loop {loop} logits")
 
 
+def test_dense_logits_stay_within_their_stride():
+    """A view whose host maxima undercount the device lengths (here: no tail counted) is
+    accepted with a stride sized to those maxima; the reader still computes every key
+    from the device lengths but writes no logit past a row's stride, so each row holds
+    the first `stride` logits of a correctly sized read and nothing beyond is touched."""
+    import ctypes as C
+
+    from flashloop_amd import _lib
+
+    print("case: dense logits stride guard B2 H3 T390", flush=True)
+    w = decode_workload(2, 3, 390, seed=14)
+    layer = _build(w)
+    lib = _lib.load()
+    kc, vc = w.current(1)
+    q, k, v = (x.to(DEV).reshape(6, 128).contiguous() for x in (w.queries[1], kc, vc))
+    view = layer.view()
+    assert view.max_tail_tokens > 0
+    stale = _lib.FlCacheView.from_buffer_copy(view)
+    stale.max_tail_tokens = 0
+    full_s = view.max_packed_tokens + view.max_tail_tokens + 1
+    s = stale.max_packed_tokens + 1
+    ref = torch.empty(6, full_s, dtype=torch.float32, device=DEV)
+    buf = torch.full((6 * s + 256,), 7.0, dtype=torch.float32, device=DEV)
+    out = torch.empty(6, 128, dtype=torch.float32, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    for vw, lg, stride in ((view, ref, full_s), (stale, buf, s)):
+        nbytes = lib.fl_decode_attn_dense_workspace(C.byref(vw))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        rc = lib.fl_decode_attn_dense(C.byref(vw), 1, q.data_ptr(), k.data_ptr(), v.data_ptr(), SCALING,
+                                      out.data_ptr(), lg.data_ptr(), stride, ws.data_ptr(), nbytes, stream)
+        assert rc == _lib.FL_OK, lib.fl_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(buf[: 6 * s].view(6, s), ref[:, :s])
+    assert bool((buf[6 * s :] == 7.0).all())
+
+
 def test_topk_bit_exact_with_ties():
     print("case: topk ties", flush=True)
     rng = np.random.default_rng(3)
