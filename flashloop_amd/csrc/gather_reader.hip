@@ -47,10 +47,12 @@ struct GatherArgs {
   float* src_out;         // source_output written (kSparseDeltaFused)
 };
 
-constexpr int kGatherSegs = 3;
-constexpr int kLenCacheG = 512;  // batches whose lengths a reader caches in LDS  // row segments a wave stages before writing partials
+constexpr int kGatherSegs = 3;   // row segments a wave stages (its first one until the end)
+constexpr int kLenCacheG = 512;  // batches whose lengths a reader caches in LDS
 
-__host__ __device__ __forceinline__ int64_t gather_slot(int w, int bh) { return static_cast<int64_t>(w) + bh; }
+// Partial slot of row bh from workgroup g: a workgroup's tile range is contiguous, so the
+// slots of one row are contiguous and disjoint from every other row's.
+__host__ __device__ __forceinline__ int64_t gather_slot(int g, int bh) { return static_cast<int64_t>(g) + bh; }
 
 // A wave-uniform 64-bit value computed on the vector unit (e.g. a division) moved to
 // scalar registers, so the values derived from it stay scalar too.
@@ -86,7 +88,10 @@ __device__ __forceinline__ float dot_bf16_words(uint4 w, const float* q) {
 // sequence (chunk = ceil(total / waves)) and runs them one after another: a tile issues
 // all its loads at once (index, then rank rows / codes / metadata) and many resident
 // waves per CU overlap each other's load latencies.  Inside a tile LPT lanes own one
-// slot (lane = LPT*n + part, 128/LPT channels per lane, T = 64/LPT slots).
+// slot (lane = LPT*n + part, 128/LPT channels per lane, T = 64/LPT slots).  The four
+// waves of a workgroup own consecutive ranges; at the end they combine their (m, l, acc)
+// of each row they share, so a row has one partial per workgroup that touched it (a
+// quarter of the parts its merge reads at batch one, where every wave runs one tile).
 //
 // K metadata is per 64-token group.  A wave keeps q*scale (per channel) and q.min (per
 // part) of the last kRing groups it loaded in a wave-private LDS ring; as its tiles walk
@@ -226,6 +231,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   __shared__ TileLds<NS, LPT> lds[kWaves];
   __shared__ float stage[kWaves][kGatherSegs][kSets][kPartial];
   __shared__ int seg_bh[kWaves][kGatherSegs];
+  __shared__ int seg_n[kWaves];
   const fl_cache_view& v = a.v;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, part = lane % LPT, n = lane / LPT;
   const int half = part / (LPT / 2);
@@ -241,12 +247,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int64_t t1 = min(t0 + chunk, total);
   const int gcap = v.token_capacity / kGroup;
 
-  auto write_stage = [&](int nseg) {
+  // Segments k0..n-1 of this wave: rows that start and end inside the wave's range, so no
+  // other wave has a partial of them (written straight to the workgroup's slot).
+  auto write_stage = [&](int k0, int n) {
     wave_sync_lds();
-    for (int k = 0; k < nseg; ++k) {
+    for (int k = k0; k < n; ++k) {
       const int sb = seg_bh[wave][k];
       for (int set = 0; set < kSets; ++set) {
-        float* dst = a.ws + (static_cast<int64_t>(set) * (a.waves + rows) + gather_slot(w, sb)) * kPartial;
+        float* dst = a.ws + (static_cast<int64_t>(set) * (a.waves + rows) + gather_slot(blockIdx.x, sb)) * kPartial;
         for (int e = lane; e < kPartial; e += kWave) dst[e] = stage[wave][k][set][e];
       }
     }
@@ -262,11 +270,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     len_cur[i] = tp + min(max(v.tail_tokens[i], 0), v.tail_capacity);
   }
   __syncthreads();
-
-  if (t0 >= t1) {
-    write_stage(0);
-    return;
-  }
 
   // Tile cursor: row, batch, tile within the row.  Cursors advance one tile at a time (an
   // integer division per tile would cost ~100 scalar instructions) and stop at the last
@@ -446,9 +449,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int bh = T.bh;
     if (bh != cur_bh) {
       if (cur_bh >= 0) {
-        if (nseg == kGatherSegs) {  // stage full: write it out (rare)
-          write_stage(nseg);
-          nseg = 0;
+        if (nseg == kGatherSegs) {  // stage full (rare): write the whole rows out, keep the first
+          write_stage(1, nseg);
+          nseg = 1;
         }
         tile_stage<LPT, MODE>(o, stage[wave][nseg][0], kSource ? stage[wave][nseg][kSets - 1] : nullptr);
         if (lane == 0) seg_bh[wave][nseg] = cur_bh;
@@ -643,6 +646,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // ---- prologue: tile t0 issued, rank rows of t0+1 and records of t0+2 in flight.  Each
   // iteration issues in age order record(j+3), rank(j+2), codes(j+1): a wait for one of
   // them never waits for younger code loads.
+  if (t0 < t1) {
   Slot s_next;
   Rec r_next;
   Tile A, B;
@@ -679,14 +683,62 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 
   if (cur_bh >= 0) {
     if (nseg == kGatherSegs) {
-      write_stage(nseg);
-      nseg = 0;
+      write_stage(1, nseg);
+      nseg = 1;
     }
     tile_stage<LPT, MODE>(o, stage[wave][nseg][0], kSource ? stage[wave][nseg][kSets - 1] : nullptr);
     if (lane == 0) seg_bh[wave][nseg] = cur_bh;
     ++nseg;
   }
-  write_stage(nseg);
+  }  // t0 < t1
+
+  // ---- the workgroup's staged segments -> one partial per row and workgroup.  A row's
+  // segments are consecutive in wave order (the waves' ranges are consecutive); each row's
+  // are combined by the whole workgroup, one thread per partial element:
+  //   m = max m_i,  l = sum l_i e^(m_i - m),  acc = sum acc_i e^(m_i - m)
+  // (sets whose m is 0 throughout, the selected-PV and aggregate sums, add up unchanged).
+  if (lane == 0) seg_n[wave] = nseg;
+  __syncthreads();
+  {
+    const int e = threadIdx.x;
+    int q0 = 0, k0 = 0;  // first entry of the next row (entries in wave order, then segment order)
+    while (q0 < kWaves && seg_n[q0] > 0) {
+      const int bh = seg_bh[q0][k0];
+      // entries of this row: (q0, k0), then the first segments of the following waves
+      int q1 = q0;
+      if (k0 == seg_n[q0] - 1)
+        while (q1 + 1 < kWaves && seg_n[q1 + 1] > 0 && seg_bh[q1 + 1][0] == bh) {
+          ++q1;
+          if (seg_n[q1] > 1) break;  // the row ends inside that wave
+        }
+      if (e < kPartial) {
+        for (int set = 0; set < kSets; ++set) {
+          auto part = [&](int q) -> const float* { return stage[q][q == q0 ? k0 : 0][set]; };
+          float m = part(q0)[0];
+          for (int q = q0 + 1; q <= q1; ++q) m = fmaxf(m, part(q)[0]);
+          float r = 0.0f;
+          for (int q = q0; q <= q1; ++q) {
+            const float* pp = part(q);
+            const float sc = pp[0] == -INFINITY ? 0.0f : fast_exp2((pp[0] - m) * kLog2e);
+            r = fmaf(sc, pp[e], r);
+          }
+          a.ws[(static_cast<int64_t>(set) * (a.waves + rows) + gather_slot(blockIdx.x, bh)) * kPartial + e] =
+              e == 0 ? m : r;
+        }
+      }
+      // next row: after the last entry used
+      if (q1 > q0) {
+        q0 = q1;
+        k0 = 1;
+      } else {
+        ++k0;
+      }
+      if (q0 < kWaves && k0 >= seg_n[q0]) {
+        ++q0;
+        k0 = 0;
+      }
+    }
+  }
 }
 
 // Merge of row bh: slots [f+bh, l+bh] of each partial set (see gather_slot).
@@ -696,7 +748,7 @@ __global__ __launch_bounds__(kMergeThreads) void gather_merge_kernel(const float
   __shared__ MergeLdsBuf S;
   const int bh = blockIdx.x, tid = threadIdx.x;
   const int64_t total = static_cast<int64_t>(nrows) * tpr;
-  const int64_t chunk = (total + waves - 1) / waves;
+  const int64_t chunk = (total + waves - 1) / waves * kWaves;  // tiles per reader workgroup
   const int64_t f = static_cast<int64_t>(bh) * tpr / chunk, l = (static_cast<int64_t>(bh + 1) * tpr - 1) / chunk;
   const int64_t o = static_cast<int64_t>(bh) * kDim + tid;
   const MergeParts P{ws + (f + bh) * kPartial, static_cast<int>(l - f + 1), nullptr};

@@ -344,6 +344,63 @@ def test_decode_step_late_loops_without_prefix_rows():
     _step_vs_oracle(w, layer, m3, m3.copy())
 
 
+def test_sparse_readers_many_rows_per_wave():
+    """5000 rows of six 8-slot tiles: a reader wave's range spans up to four rows (its
+    whole middle rows leave its staging early) and rows are split between the waves of a
+    workgroup, whose partials of one row are combined before the merge.  Selected-PV sums,
+    the fused loop-3 delta with its loop-2 aggregate and the loop-4 delta, against torch
+    over the pack's reconstructed rows (pinned to the oracle by the pack tests)."""
+    print("case: sparse readers B625 H8 T130 capacity 48", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    B, H, T, cap = 625, 8, 130, 48
+    R = B * H
+    bf = torch.bfloat16
+    keys = [torch.randn(B, H, T, 128, device=DEV, generator=g).to(bf) for _ in range(4)]
+    values = [torch.randn(B, H, T, 128, device=DEV, generator=g).to(bf) for _ in range(4)]
+    layer = CrossLoopKVLayer.from_prefill(keys, values, recon=True)
+    tp = layer.quantized_tokens
+    assert tp == 64 and layer.tail_host[0] == T - tp
+    cur_k = [torch.randn(B, H, 1, 128, device=DEV, generator=g).to(bf) for _ in range(4)]
+    cur_v = [torch.randn(B, H, 1, 128, device=DEV, generator=g).to(bf) for _ in range(4)]
+    q = [torch.randn(B, H, 1, 128, device=DEV, generator=g).to(bf) for _ in range(4)]
+    # cap sorted distinct indices per row among the T + 1 keys (index T: the current token)
+    idx = torch.argsort(torch.rand(R, T + 1, device=DEV, generator=g), dim=1)[:, :cap].sort(dim=1).values
+    valid = (torch.rand(R, cap, device=DEV, generator=g) > 0.1).to(torch.uint8)
+    w = torch.rand(R, cap, device=DEV, generator=g) * valid
+    w = w / w.sum(dim=1, keepdim=True)
+
+    def rows(loop, recon, src, cur):  # [R, T + 1, 128] f32: prefix, tail, current token
+        return torch.cat([recon[loop][:, :tp].float(), src[loop].reshape(R, T, 128)[:, tp:].float(),
+                          cur[loop].reshape(R, 1, 128).float()], dim=1)
+
+    def pick(x):
+        return x.gather(1, idx.long()[..., None].expand(-1, -1, 128))
+
+    def softmax_pv(loop):
+        kr, vr = pick(rows(loop, layer.recon_keys, keys, cur_k)), pick(rows(loop, layer.recon_values, values, cur_v))
+        lg = torch.einsum("rjc,rc->rj", kr, q[loop].reshape(R, 128).float()) * SCALING
+        lg = lg.masked_fill(valid == 0, -float("inf"))
+        return torch.einsum("rj,rjc->rc", torch.softmax(lg, dim=1), vr)
+
+    v1 = pick(rows(1, layer.recon_values, values, cur_v))
+    want_so = torch.einsum("rj,rjc->rc", w, v1)
+    so = layer.pv(1, w, idx.int(), valid, cur_v[1])
+    torch.cuda.synchronize()
+    assert_close(np32(so).reshape(R, 128), np32(want_so), what="selected PV, loop 2")
+    mass = torch.rand(R, device=DEV, generator=g) + 0.5
+    d2, so2 = layer.cached_mass_sparse_attention_delta_with_source(
+        2, query=q[2], current_key=cur_k[2], current_value=cur_v[2], indices=idx.int(), valid=valid,
+        source_weights=w, source_current_value=cur_v[1], global_mass=mass, scaling=SCALING)
+    d3 = layer.cached_mass_sparse_attention_delta(
+        3, query=q[3], current_key=cur_k[3], current_value=cur_v[3], indices=idx.int(), valid=valid,
+        source_selected_output=so2, global_mass=mass, scaling=SCALING)
+    torch.cuda.synchronize()
+    assert_close(np32(so2).reshape(R, 128), np32(want_so), what="fused loop-2 aggregate")
+    for loop, got in ((2, d2), (3, d3)):
+        want = mass[:, None] * (softmax_pv(loop) - so2.reshape(R, 128))
+        assert_close(np32(got).reshape(R, 128), np32(want), what=f"loop-{loop + 1} delta")
+
+
 def test_decode_step_ragged_batch():
     print("case: decode step ragged B3 H2", flush=True)
     lengths = ragged_lengths(3, 100, 900, seed=2)
