@@ -647,50 +647,50 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // iteration issues in age order record(j+3), rank(j+2), codes(j+1): a wait for one of
   // them never waits for younger code loads.
   if (t0 < t1) {
-  Slot s_next;
-  Rec r_next;
-  Tile A, B;
-  Pos pr = pos_at(t0);  // cursor of the next selection record to load
-  Pos ps = pr;          // cursor of the next slot to resolve
-  {
-    const Rec r0 = load_rec(pr);
-    step(pr);
-    const Rec r1 = load_rec(pr);
-    step(pr);
-    r_next = load_rec(pr);
-    const Slot s0 = resolve(ps, r0);
-    step(ps);
-    s_next = resolve(ps, r1);
-    A = issue(s0);
-  }
-
-  for (int64_t tile = t0;;) {
-    step(pr);
-    step(ps);
-    Rec r3 = load_rec(pr);           // selection record of tile+3
-    Slot s2 = resolve(ps, r_next);   // rank rows of tile+2
-    B = issue(s_next);               // codes of tile+1
-    compute(A);
-    if (++tile >= t1) break;
-    step(pr);
-    step(ps);
-    r_next = load_rec(pr);
-    s_next = resolve(ps, r3);
-    A = issue(s2);
-    compute(B);
-    if (++tile >= t1) break;
-  }
-
-  if (cur_bh >= 0) {
-    if (nseg == kGatherSegs) {
-      write_stage(1, nseg);
-      nseg = 1;
+    Slot s_next;
+    Rec r_next;
+    Tile A, B;
+    Pos pr = pos_at(t0);  // cursor of the next selection record to load
+    Pos ps = pr;          // cursor of the next slot to resolve
+    {
+      const Rec r0 = load_rec(pr);
+      step(pr);
+      const Rec r1 = load_rec(pr);
+      step(pr);
+      r_next = load_rec(pr);
+      const Slot s0 = resolve(ps, r0);
+      step(ps);
+      s_next = resolve(ps, r1);
+      A = issue(s0);
     }
-    tile_stage<LPT, MODE>(o, stage[wave][nseg][0], kSource ? stage[wave][nseg][kSets - 1] : nullptr);
-    if (lane == 0) seg_bh[wave][nseg] = cur_bh;
-    ++nseg;
+
+    for (int64_t tile = t0;;) {
+      step(pr);
+      step(ps);
+      Rec r3 = load_rec(pr);           // selection record of tile+3
+      Slot s2 = resolve(ps, r_next);   // rank rows of tile+2
+      B = issue(s_next);               // codes of tile+1
+      compute(A);
+      if (++tile >= t1) break;
+      step(pr);
+      step(ps);
+      r_next = load_rec(pr);
+      s_next = resolve(ps, r3);
+      A = issue(s2);
+      compute(B);
+      if (++tile >= t1) break;
+    }
+
+    if (cur_bh >= 0) {
+      if (nseg == kGatherSegs) {
+        write_stage(1, nseg);
+        nseg = 1;
+      }
+      tile_stage<LPT, MODE>(o, stage[wave][nseg][0], kSource ? stage[wave][nseg][kSets - 1] : nullptr);
+      if (lane == 0) seg_bh[wave][nseg] = cur_bh;
+      ++nseg;
+    }
   }
-  }  // t0 < t1
 
   // ---- the workgroup's staged segments -> one partial per row and workgroup.  A row's
   // segments are consecutive in wave order (the waves' ranges are consecutive); each row's
