@@ -90,7 +90,12 @@ class CrossLoopKVLayer:
         # host mirrors (no device sync on the decode path)
         self.packed_host = [0] * g.batch
         self.tail_host = [0] * g.batch
-        self.late_rows_host = [[0] * g.batch, [0] * g.batch]
+        # host mirror of late_rows, read back lazily: a rollover advances the device counts
+        # without a sync and adds GROUP per rolled group to _late_pending, an upper bound
+        # of what the mirror is missing (enough for the capacity check)
+        self._late_rows_host = [[0] * g.batch, [0] * g.batch]
+        self._late_pending = [[0] * g.batch, [0] * g.batch]
+        self._late_stale = False
         self._view: FlCacheView | None = None
         self.workspace = kernels.Workspace()
 
@@ -106,6 +111,21 @@ class CrossLoopKVLayer:
     @property
     def rows(self) -> int:
         return self.batch * self.heads
+
+    @property
+    def late_rows_host(self) -> list[list[int]]:
+        """Rows used in streams 2/3 per sequence (host mirror of ``late_rows``)."""
+        if self._late_stale:
+            self._late_rows_host = [[int(x) for x in r] for r in self.late_rows.tolist()]
+            self._late_pending = [[0] * self.batch, [0] * self.batch]
+            self._late_stale = False
+        return self._late_rows_host
+
+    @late_rows_host.setter
+    def late_rows_host(self, rows: list[list[int]]) -> None:
+        self._late_rows_host = rows
+        self._late_pending = [[0] * self.batch, [0] * self.batch]
+        self._late_stale = False
 
     @property
     def quantized_tokens(self) -> int:
@@ -371,10 +391,12 @@ class CrossLoopKVLayer:
     def _roll_groups(self) -> None:
         """``_roll_one_group`` (flashloop/cache.py:1778-1838) for every sequence whose tail
         holds residual+group rows: pack tail rows [0, 64) as prefix group Tp/64, then shift
-        the tail down by 64.  O(group): the prefix is never re-read."""
+        the tail down by 64.  O(group): the prefix is never re-read.  Every step is a device
+        op on device counts (no host read-back), unless the loop-3/4 row capacity could be
+        exhausted, which is then checked exactly."""
         b, h = self.batch, self.heads
+        dev = self.device
         roll = [x >= self.residual_length + GROUP for x in self.tail_host]
-        g0 = [self.packed_host[i] // GROUP if roll[i] else -1 for i in range(b)]
         for i in range(b):
             if roll[i] and self.packed_host[i] + GROUP > self.geometry.token_capacity:
                 raise RuntimeError("packed prefix capacity exhausted; allocate a larger token_capacity")
@@ -384,16 +406,20 @@ class CrossLoopKVLayer:
                 if not roll[i]:
                     continue
                 act = self.tail_active[s][i, :GROUP].bool()
-                n_act = int(act.sum().item())
-                base = self.late_rows_host[s][i]
-                if base + n_act > self.geometry.row_capacity[s + 2]:
-                    raise RuntimeError("loop-3/4 row capacity exhausted")
-                r = torch.cumsum(act.to(torch.int32), 0) - 1 + base
-                r = torch.where(act, r, torch.full_like(r, -1)).to(torch.int32)
+                cap = self.geometry.row_capacity[s + 2]
+                if self._late_rows_host[s][i] + self._late_pending[s][i] + GROUP > cap:
+                    if self.late_rows_host[s][i] + int(act.sum().item()) > cap:  # exact (reads back)
+                        raise RuntimeError("loop-3/4 row capacity exhausted")
+                r = torch.cumsum(act.to(torch.int32), 0) - 1 + self.late_rows[s, i]
                 p = self.packed_host[i]
-                self.rank[s][i, p : p + GROUP] = r
-                self.late_rows_host[s][i] = base + n_act
-        dst = torch.tensor(g0, dtype=torch.int32, device=self.device)
+                self.rank[s][i, p : p + GROUP] = torch.where(act, r, torch.full_like(r, -1))
+                self.late_rows[s, i] += act.sum(dtype=torch.int32)
+                self._late_pending[s][i] += GROUP
+                self._late_stale = True
+        dst = torch.full((b,), -1, dtype=torch.int32, device=dev)
+        for i in range(b):
+            if roll[i]:
+                dst[i] = self.packed_host[i] // GROUP
         kernels.pack_kv_groups(
             self.view(), 4, self.tail_key, self.tail_value, src_bh_stride=self.geometry.tail_capacity,
             src_row_offset=0, dst_group0=dst, n_groups=1, masks=self.tail_active,
@@ -404,16 +430,18 @@ class CrossLoopKVLayer:
                 continue
             rows = slice(i * h, (i + 1) * h)
             n = self.tail_host[i] - GROUP
+            # rows [GROUP, GROUP + n) -> [0, n): disjoint ranges (no copy first) when n <= GROUP
+            def shift(src):
+                return src if n <= GROUP else src.clone()
             for tensor in (*self.tail_key, *self.tail_value):
-                tensor[rows, :n] = tensor[rows, GROUP : GROUP + n].clone()
+                tensor[rows, :n] = shift(tensor[rows, GROUP : GROUP + n])
             for act in self.tail_active:
-                act[i, :n] = act[i, GROUP : GROUP + n].clone()
+                act[i, :n] = shift(act[i, GROUP : GROUP + n])
                 act[i, n:] = 0
             self.packed_host[i] += GROUP
             self.tail_host[i] = n
-        self.packed_tokens.copy_(torch.tensor(self.packed_host, dtype=torch.int32))
-        self.tail_tokens.copy_(torch.tensor(self.tail_host, dtype=torch.int32))
-        self.late_rows.copy_(torch.tensor(self.late_rows_host, dtype=torch.int32))
+            self.packed_tokens[i] += GROUP
+            self.tail_tokens[i] -= GROUP
 
     # ------------------------------------------------------------------ serialization
     # On-disk format (FORMAT_NAME, FORMAT_VERSION): one safetensors file whose tensors are
