@@ -36,8 +36,9 @@ COMMON_FLAGS = [
     "-packed-fp32-ops",
     f"-I{PKG.parent / 'include'}",
 ]
-# the codec must never contract a*b+c into an FMA: its reference rounds each op
-PER_FILE_FLAGS = {"pack.hip": ["-ffp-contract=off"]}
+# the codec must never contract a*b+c into an FMA: its reference rounds each op; the
+# top-k's softmax weight image is reproduced bit for bit on the CPU
+PER_FILE_FLAGS = {"pack.hip": ["-ffp-contract=off"], "topk.hip": ["-ffp-contract=off"]}
 
 
 def _hipcc() -> str:
@@ -59,11 +60,18 @@ def _compile(src: Path, hipcc: str, extra: list[str]) -> Path:
     return obj
 
 
+# Extra hipcc flags a caller may add: diagnostics only, none changes the generated code.
+ALLOWED_EXTRA_FLAGS = frozenset({"-Rpass-analysis=kernel-resource-usage", "-save-temps"})
+
+
 def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     hipcc = _hipcc()
+    extra = list(extra_flags or [])
+    bad = [f for f in extra if f not in ALLOWED_EXTRA_FLAGS]
+    if bad:
+        raise ValueError(f"flags not allowed in the library build: {bad} (allowed: {sorted(ALLOWED_EXTRA_FLAGS)})")
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    extra = list(extra_flags or [])
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         objs = list(ex.map(lambda s: _compile(s, hipcc, extra), sources))
     tmp = LIB.with_suffix(".so.tmp")

@@ -400,16 +400,21 @@ class CrossLoopKVLayer:
         for i in range(b):
             if roll[i] and self.packed_host[i] + GROUP > self.geometry.token_capacity:
                 raise RuntimeError("packed prefix capacity exhausted; allocate a larger token_capacity")
+        # every capacity check runs before the first device change, so a refused rollover
+        # leaves the rank maps and device row counts as they were
+        for s in range(2):
+            cap = self.geometry.row_capacity[s + 2]
+            for i in range(b):
+                if roll[i] and self._late_rows_host[s][i] + self._late_pending[s][i] + GROUP > cap:
+                    act_n = int(self.tail_active[s][i, :GROUP].sum().item())
+                    if self.late_rows_host[s][i] + act_n > cap:  # exact (reads back)
+                        raise RuntimeError("loop-3/4 row capacity exhausted")
         # rank maps of the new group's rows (active rows continue the compact numbering)
         for s in range(2):
             for i in range(b):
                 if not roll[i]:
                     continue
                 act = self.tail_active[s][i, :GROUP].bool()
-                cap = self.geometry.row_capacity[s + 2]
-                if self._late_rows_host[s][i] + self._late_pending[s][i] + GROUP > cap:
-                    if self.late_rows_host[s][i] + int(act.sum().item()) > cap:  # exact (reads back)
-                        raise RuntimeError("loop-3/4 row capacity exhausted")
                 r = torch.cumsum(act.to(torch.int32), 0) - 1 + self.late_rows[s, i]
                 p = self.packed_host[i]
                 self.rank[s][i, p : p + GROUP] = torch.where(act, r, torch.full_like(r, -1))

@@ -374,33 +374,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       // row base (scalar) + line offset (32-bit: row < row_capacity < 2^24)
       const int64_t base = static_cast<int64_t>(sl.bh) * v.row_capacity[s] * kCodeStride;
       const uint32_t off = static_cast<uint32_t>(row[s]) * kCodeStride + 4 * kWords * part;
-#ifdef FL_GATHER_NOLOAD
-      // measurement build only: the code words come from the slot's token instead of
-      // memory (index and rank loads stay), so a run times the arithmetic's chains
-      for (int k = 0; k < kWords; ++k) {
-        T.kw[s][k] = static_cast<uint32_t>(sl.t) * 2654435761u + 97u * s + 13u * k + off;
-        T.vw[s][k] = static_cast<uint32_t>(sl.t) * 40503u + 31u * s + 7u * k + off;
-      }
-      (void)base;
-#else
       if (kSoftmax) load_words<LPT>(T.kw[s], v.key_codes[s] + base + off);
       load_words<LPT>(T.vw[s], v.key_codes[s] + base + off + kCodeStride / 2);  // V row: second half of the line
-#endif
     }
     // V metadata of every stream from the token's 64-byte record (this lane's half: 32 bytes)
     const float* rec = v.value_meta_token + static_cast<int64_t>(sl.bh) * v.token_capacity * 16;
     const uint32_t roff = static_cast<uint32_t>(pre ? sl.t : 0) * 64u + half * 32u;
-#ifdef FL_GATHER_NOLOAD
-    {
-      const float f = static_cast<float>(roff & 1023u) * 1e-4f;
-      T.vm01 = make_float4(0.01f + f, f, 0.02f + f, f);
-      T.vm23 = make_float4(0.03f + f, f, 0.04f + f, f);
-      (void)rec;
-    }
-#else
     T.vm01 = load_at<float4>(rec, roff);
     T.vm23 = NS > 2 ? load_at<float4>(rec, roff + 16u) : make_float4(0.f, 0.f, 0.f, 0.f);
-#endif
     T.glo = 0;
     T.nnew = 0;
     T.gfirst = 0;
@@ -426,12 +407,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         if (j < T.nnew)
 #pragma unroll
           for (int s = 0; s < NS; ++s)
-#ifdef FL_GATHER_NOLOAD
-            T.km[j][s] = make_uint2(0x2C003C00u + static_cast<uint32_t>(T.glo + j + s) * 3u, 0x1C00u + lane);
-#else
             T.km[j][s] = load_at<uint2>(v.key_meta_half[s] + (static_cast<int64_t>(sl.bh) * gcap + T.glo + j) * kDim * 2,
                                         8u * lane);
-#endif
       T.qw = load_at<uint32_t>(a.q + static_cast<int64_t>(sl.bh) * kDim, 4u * lane);
     }
     return T;
@@ -472,27 +449,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         qe = ldexpf(kSub16, e);
       }
     }
-#ifdef FL_GATHER_NOCOMPUTE
-    // Measurement build only (never the default): the tile's arithmetic is replaced by
-    // folding every loaded word into one register, so a run of this build times the
-    // access pattern and pipeline alone.  Outputs are meaningless.
-    {
-      uint32_t x = T.qw ^ __float_as_uint(T.vm01.x) ^ __float_as_uint(T.vm23.y) ^ static_cast<uint32_t>(T.t);
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-#pragma unroll
-        for (int k = 0; k < kWords; ++k) x ^= T.kw[s][k] ^ T.vw[s][k];
-      if (kSoftmax)
-#pragma unroll
-        for (int j = 0; j < kNew; ++j)
-          if (j < T.nnew)
-#pragma unroll
-            for (int s = 0; s < NS; ++s) x ^= T.km[j][s].x ^ T.km[j][s].y;
-      o.acc[0] += static_cast<float>(x & 7u);
-      o.l += 1.0f;
-      return;
-    }
-#endif
     const int t = T.t, Tp = T.Tp, cur = T.cur;
     const uint32_t has = T.has;
     const bool pre = t >= 0 && t < Tp;
@@ -831,10 +787,7 @@ int gather_occupancy() {
 
 constexpr int kGatherMaxResident = 4;  // workgroups per CU any reader instantiation holds
 
-#ifndef FL_GATHER_LPT
-#define FL_GATHER_LPT 8
-#endif
-constexpr int kLpt = FL_GATHER_LPT;  // lanes per selected slot
+constexpr int kLpt = 8;  // lanes per selected slot
 
 // Persistent grid: one wave per tile up to every resident workgroup slot (a small
 // selection, e.g. batch one, gets one tile per wave: its waves are latency chains).
@@ -852,11 +805,7 @@ size_t gather_workspace(int rows, int capacity) {
 
 template <int NS, int MODE>
 void launch_ns(GatherArgs& a, int rows, hipStream_t st) {
-#ifdef FL_GATHER_OCC  // measurement build only: resident workgroups per CU forced
-  const int blocks = gather_blocks(rows, a.cap, FL_GATHER_OCC);
-#else
   const int blocks = gather_blocks(rows, a.cap, gather_occupancy<NS, MODE, kLpt>());
-#endif
   a.waves = blocks * kWaves;
   a.tpr = a.cap / Lay<kLpt>::kTok;
   hipLaunchKernelGGL((gather_reader_kernel<NS, MODE, kLpt>), dim3(blocks), dim3(kThreads), 0, st, a);

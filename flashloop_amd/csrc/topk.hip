@@ -36,6 +36,71 @@ __device__ __forceinline__ float key_value(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
 }
 
+// ---- Ranking key of the decode selection: the fp32 softmax weight.
+// flashloop/engine.py:439-453 ranks w = softmax(logits, dtype=float32) with torch.topk
+// (selection.py:85 likewise), so distinct logits whose weights round to one fp32 value tie
+// there -- e.g. every key whose weight underflows to 0 in a peaked row -- and the tie goes
+// to the lower index.  The kernels rank the same image:
+//   e = softmax_exp(RN(x - max)),  Z = row_weight_sum(e),  w = RN(e * RN(1/Z)),
+// key = bits(w) + 1 (w >= 0, so the bits order like the values; key 0 marks padding).
+// softmax_exp uses IEEE fma/mul only and Z has a fixed summation order, so every bit of
+// w is reproducible on the CPU.  This file is compiled with -ffp-contract=off.
+constexpr float kInvLn2 = 0x1.715476p+0f;   // RN(1/ln 2)
+constexpr float kLn2Hi = 0x1.62e430p-1f;    // RN(ln 2)
+constexpr float kLn2Lo = -0x1.05c610p-29f;  // RN(ln 2 - kLn2Hi)
+
+// exp(d) for d <= 0 (d = -inf gives 0): Cody-Waite reduction d = n ln2 + r, |r| <= ln2/2,
+// the degree-7 Taylor polynomial of e^r by Horner (truncation 5e-9 relative), and the
+// scale 2^n applied as an exact multiply by 2^(n+64) and a rounding multiply by 2^-64,
+// so a result in the subnormal range is rounded once.  Within ~2 ulp of exp.
+__device__ __forceinline__ float softmax_exp(float d) {
+  d = fmaxf(d, -112.0f);  // exp(-112) rounds to 0 as every smaller argument does
+  const float n = rintf(d * kInvLn2);
+  float r = fmaf(n, -kLn2Hi, d);
+  r = fmaf(n, -kLn2Lo, r);
+  float p = 0x1.a01a02p-13f;      // 1/7!
+  p = fmaf(p, r, 0x1.6c16c2p-10f);  // 1/6!
+  p = fmaf(p, r, 0x1.111112p-7f);   // 1/5!
+  p = fmaf(p, r, 0x1.555556p-5f);   // 1/4!
+  p = fmaf(p, r, 0x1.555556p-3f);   // 1/3!
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  const float up = __uint_as_float(static_cast<uint32_t>(static_cast<int>(n) + 64 + 127) << 23);  // 2^(n+64)
+  const float e = p * up;
+  return e * 0x1p-64f;
+}
+
+// w = RN(e * invZ) as a ranking key (>= 1)
+__device__ __forceinline__ uint32_t weight_key(float e, float invZ) { return __float_as_uint(e * invZ) + 1u; }
+__device__ __forceinline__ float key_weight(uint32_t key) { return __uint_as_float(key - 1u); }
+// key of a row that holds NaN or +inf (its softmax is NaN throughout): the score order,
+// -inf ranked as -FLT_MAX, every key >= 1
+constexpr uint32_t kScoreKeyFloor = 0x00800000u;  // order_key(-FLT_MAX)
+__device__ __forceinline__ uint32_t score_key(float x) { return max(order_key(x), kScoreKeyFloor); }
+
+// Sum over a wave in a fixed order: pairs at lane distance 32, 16, ..., 1 (every lane ends
+// with the same bits: a + b and b + a round alike).
+__device__ __forceinline__ float wave_sum_fixed(float v) {
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Sum over the workgroup in a fixed order: wave_sum_fixed, then the 16 wave sums in wave
+// order.
+template <typename Sh>
+__device__ float res_block_sum_fixed(float v, Sh& sh) {
+  v = wave_sum_fixed(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh.red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sh.red[0];
+#pragma unroll
+  for (int i = 1; i < kTopkWaves; ++i) r += sh.red[i];
+  return r;
+}
+
 struct TopkShared {
   uint32_t hist[256];
   uint32_t wave_cnt[kTopkWaves];
@@ -69,10 +134,11 @@ __device__ float block_sum(float v, TopkShared& sh) {
   return r;
 }
 
-// Radix-select the k-th largest candidate key of the row.  On return (all threads):
-// *kth = K*, *need = number of keys equal to K* to take (taking lowest indices first).
-template <typename Cand>
-__device__ void radix_select(const float* x, int n, int k, Cand cand, TopkShared& sh, uint32_t* kth, int* need) {
+// Radix-select the k-th largest candidate key (key(i): the ranking key of index i) of the
+// row.  On return (all threads): *kth = K*, *need = number of keys equal to K* to take
+// (taking lowest indices first).
+template <typename Key, typename Cand>
+__device__ void radix_select(Key key_of, int n, int k, Cand cand, TopkShared& sh, uint32_t* kth, int* need) {
   uint32_t prefix = 0, mask = 0;
   int remaining = k;
   for (int shift = 24; shift >= 0; shift -= 8) {
@@ -80,7 +146,7 @@ __device__ void radix_select(const float* x, int n, int k, Cand cand, TopkShared
     __syncthreads();
     for (int i = threadIdx.x; i < n; i += kTopkThreads) {
       if (!cand(i)) continue;
-      const uint32_t key = order_key(x[i]);
+      const uint32_t key = key_of(i);
       if ((key & mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 0xFFu], 1u);
     }
     __syncthreads();
@@ -120,18 +186,19 @@ __device__ void radix_select(const float* x, int n, int k, Cand cand, TopkShared
   *need = remaining;
 }
 
-// Walk the row in index order; call emit(i, out_pos) for every selected candidate.
+// Walk the row in index order; call emit(i, out_pos, key) for every selected candidate.
 // Returns the number selected.
-template <typename Cand, typename Emit>
-__device__ int compact_selected(const float* x, int n, uint32_t kth, int need, Cand cand, TopkShared& sh, Emit emit) {
+template <typename Key, typename Cand, typename Emit>
+__device__ int compact_selected(Key key_of, int n, uint32_t kth, int need, Cand cand, TopkShared& sh, Emit emit) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   int eq_base = 0, out_base = 0;
   for (int base = 0; base < n; base += kTopkThreads) {
     const int i = base + threadIdx.x;
     bool gt = false, eq = false;
+    uint32_t key = 0;
     if (i < n && cand(i)) {
-      const uint32_t key = order_key(x[i]);
+      key = key_of(i);
       gt = key > kth;
       eq = key == kth;
     }
@@ -156,7 +223,7 @@ __device__ int compact_selected(const float* x, int n, uint32_t kth, int need, C
       if (j < w) pos += c;
       sel_total += c;
     }
-    if (sel) emit(i, pos);
+    if (sel) emit(i, pos, key);
     eq_base += eq_total;
     out_base += sel_total;
     __syncthreads();
@@ -200,27 +267,42 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
     }
     return;
   }
-  // softmax statistics of the row (flashloop/engine.py:440-442)
+  // softmax statistics of the row (flashloop/engine.py:440-442) and its non-finite scores
   if (threadIdx.x == 0) sh.nonfin = 0;
   float mx = -INFINITY;
-  uint32_t nf = 0;
+  uint32_t nf = 0, amax = 0;
   for (int i = threadIdx.x; i < n; i += kTopkThreads) {
-    mx = fmaxf(mx, x[i]);
-    nf += non_finite(x[i]) ? 1u : 0u;
+    const float xi = x[i];
+    mx = fmaxf(mx, xi);
+    amax = max(amax, __float_as_uint(xi) & 0x7FFFFFFFu);
+    nf += non_finite(xi) ? 1u : 0u;
   }
   const float M = block_max(mx, sh);  // (its barriers order the counter's reset)
   if (nf) atomicAdd(&sh.nonfin, nf);
-  float z = 0.0f;
-  for (int i = threadIdx.x; i < n; i += kTopkThreads) z += fast_exp2((x[i] - M) * kLog2e);
-  const float Z = block_sum(z, sh);
-  const float invZ = 1.0f / Z;
+  // NaN anywhere is flagged through the count of keys above inf's bits
+  if (amax > 0x7F800000u) atomicOr(&sh.nonfin, 0x40000000u);
+  __syncthreads();
+  const bool weighted = (sh.nonfin & 0x40000000u) == 0u && M > -INFINITY && M < INFINITY;
+  __syncthreads();
+  if (threadIdx.x == 0) sh.nonfin &= 0x3FFFFFFFu;
+  // the same weight image and summation order as the register-resident kernel: thread t
+  // sums indices t, t + 1024, ... in order, then the fixed-order block sum
+  float invZ = 0.0f;
+  if (weighted) {
+    float z = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kTopkThreads) z += softmax_exp(x[i] - M);
+    invZ = 1.0f / res_block_sum_fixed(z, sh);
+  }
+  const auto key_of = [&](int i) {
+    return weighted ? weight_key(softmax_exp(x[i] - M), invZ) : score_key(x[i]);
+  };
 
   uint32_t kth;
   int need;
-  radix_select(x, n, k, AllCand{}, sh, &kth, &need);
+  radix_select(key_of, n, k, AllCand{}, sh, &kth, &need);
   float msum = 0.0f;
-  compact_selected(x, n, kth, need, AllCand{}, sh, [&](int i, int pos) {
-    const float w = fast_exp2((x[i] - M) * kLog2e) * invZ;
+  compact_selected(key_of, n, kth, need, AllCand{}, sh, [&](int i, int pos, uint32_t key) {
+    const float w = weighted ? key_weight(key) : NAN;
     oi[pos] = i;
     ov[pos] = 1;
     ow[pos] = w;
@@ -229,10 +311,9 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
   const float S = block_sum(msum, sh);
   __threadfence_block();
   __syncthreads();
-  const float invS = 1.0f / S;
   for (int j = threadIdx.x; j < cap; j += kTopkThreads) {
     if (j < k) {
-      ow[j] = ow[j] * invS;
+      ow[j] = ow[j] / S;  // selected_global / mass (engine.py:492)
     } else {
       oi[j] = 0;
       ov[j] = 0;
@@ -277,8 +358,6 @@ __device__ __forceinline__ int value_bin(float x, float inv, float off) {
   const float b = fminf(fmaxf(fmaf(x, inv, off), 0.0f), static_cast<float>(kBins - 1));
   return static_cast<int>(b);
 }
-
-constexpr uint32_t kPadKey = 0x007FFFFFu;  // order_key(-inf)
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
@@ -432,57 +511,74 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     return;
   }
 
-  // ---- 1. load (slot j of thread t is index j * 1024 + t).  Slots past n hold kPadKey,
-  // the key of -inf, and real keys are clamped above it (a -inf score ranks as -FLT_MAX):
-  // padding then adds 0 to the normaliser, lands in bin 0 (whose count is corrected), is
-  // never a boundary candidate and never compares above the k-th key, so no later pass
-  // needs an index test.
-  uint32_t kr[PER];
+  // ---- 1. load (slot j of thread t is index j * 1024 + t), row max and min, and what
+  // kinds of non-finite score the row holds (the max of |x|'s bits: > inf's bits is NaN)
+  uint32_t kr[PER];  // the score bits, then e's bits, then the ranking key (0 = padding)
   float mx = -INFINITY, mn = INFINITY;
+  uint32_t amax = 0;
   if (tid == 0) sh.nonfin = 0;
-  float chk = 0.0f;  // x*0 summed: 0 unless some score is NaN or +-inf
   {
     float xs[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = j * kTopkThreads + tid;
-      xs[j] = (i < n) ? x[i] : 0.0f;
+      xs[j] = (i < n) ? x[i] : -INFINITY;
     }
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const bool in = j * kTopkThreads + tid < n;
-      kr[j] = in ? max(order_key(xs[j]), kPadKey + 1u) : kPadKey;
-      chk = fmaf(xs[j], 0.0f, chk);  // (xs[j] is 0 past n)
-      if (in) {
-        mx = fmaxf(mx, xs[j]);
-        mn = fminf(mn, xs[j]);
-      }
+      kr[j] = __float_as_uint(xs[j]);
+      amax = max(amax, in ? kr[j] & 0x7FFFFFFFu : 0u);
+      mx = fmaxf(mx, xs[j]);
+      mn = fminf(mn, in ? xs[j] : INFINITY);
     }
   }
   for (int i = tid; i < kBins; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
   if (tid == 0) sh.ncand = 0;
-  const float3 ext = res_block_max3(mx, -mn, chk != 0.0f ? 1.0f : 0.0f, sh);  // (its barriers order the reset)
+  // flag 2: a NaN; flag 1: an infinity
+  const float flag = amax > 0x7F800000u ? 2.0f : (amax == 0x7F800000u ? 1.0f : 0.0f);
+  const float3 ext = res_block_max3(mx, -mn, flag, sh);  // (its barriers order the reset)
   const float M = ext.x;
   mn = -ext.y;
-  const bool badrow = ext.z != 0.0f;
-  // bin(x) = clamp(x * inv - mn * inv); non-finite extremes collapse every key into bin 0
-  // (the crowded-bin fallback then covers all)
-  const float inv = (isfinite(M) && isfinite(mn) && M > mn) ? static_cast<float>(kBins) / (M - mn) : 0.0f;
-  const float off = -mn * inv;
-  const float mlog = M * kLog2e;
+  // softmax weights exist unless the row holds a NaN or +inf, or only -inf (then torch's
+  // fp32 softmax is NaN throughout and the score order ranks instead)
+  const bool weighted = ext.z < 2.0f && M > -INFINITY && M < INFINITY;
+  const bool badrow = ext.z != 0.0f;  // some score may be non-finite: counted below
 
-  // ---- 2. normaliser and value histogram
-  float z = 0.0f;
+  // ---- 2. the weight image (weighted rows) or the score order, as keys
+  float invZ = 0.0f;
+  uint32_t kmin = kScoreKeyFloor, shift = 31u, binmax = 0u;  // a score-ordered row: one bin
+  if (weighted) {
+    float z = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float e = softmax_exp(__uint_as_float(kr[j]) - M);
+      z += e;
+      kr[j] = __float_as_uint(e);
+    }
+    const float Z = res_block_sum_fixed(z, sh);
+    invZ = 1.0f / Z;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) kr[j] = (j * kTopkThreads + tid < n) ? weight_key(__uint_as_float(kr[j]), invZ) : 0u;
+    // keys lie in [key(min score), key(max score) = bits(invZ) + 1]; bins of 2^shift keys
+    kmin = weight_key(softmax_exp(mn - M), invZ);
+    const uint32_t span = max(__float_as_uint(invZ) + 1u, kmin) - kmin;
+    shift = span < static_cast<uint32_t>(kBins) ? 0u : 32u - static_cast<uint32_t>(__clz(span)) - 10u;
+    binmax = kBins - 1;
+  } else {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) kr[j] = (j * kTopkThreads + tid < n) ? score_key(__uint_as_float(kr[j])) : 0u;
+  }
+
+  // ---- 3. value histogram: bin(key) is non-decreasing in the key (and 0 for padding)
   uint32_t* lin = &sh.hist[0][0];  // one kBins-bin histogram (the sub-histograms are for the radix)
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const float xi = key_value(kr[j]);
-    z += fast_exp2(fmaf(xi, kLog2e, -mlog));
-    const int b = value_bin(xi, inv, off);
+    const int b = static_cast<int>(min(static_cast<uint32_t>(max(static_cast<int>(kr[j] - kmin), 0)) >> shift, binmax));
     sh.bin[j][tid] = static_cast<uint16_t>(b);
     atomicAdd(&lin[b], 1u);
   }
-  const float Z = res_block_sum(z, sh);  // (its barriers also complete the histogram)
+  __syncthreads();  // the histogram is complete
   // Only a row holding a non-finite score (the same decision in every thread) counts
   // them, re-reading the row.
   if (badrow) {
@@ -520,7 +616,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     const int i = j * kTopkThreads + tid;
     const int b = sh.bin[j][tid];
     const uint64_t bal_a = ballot64(b > bstar);
-    const bool in_b = b == bstar && kr[j] != kPadKey;
+    const bool in_b = b == bstar && kr[j] != 0u;
     const uint64_t bal_b = ballot64(in_b);
     cnt_lane = lane == j ? static_cast<uint32_t>(__popcll(bal_a)) : cnt_lane;
     if (bal_b != 0ull) {
@@ -581,7 +677,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         const uint32_t kk = kr[j];
-        if (kk != kPadKey && (kk & pmask) == prefix && static_cast<int>(sh.bin[j][tid]) == bstar)
+        if (kk != 0u && (kk & pmask) == prefix && static_cast<int>(sh.bin[j][tid]) == bstar)
           atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
       }
       __syncthreads();
@@ -671,7 +767,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
   __syncthreads();
 
   // ---- 5. weights of the k selected keys, coalesced output
-  const float invZ = 1.0f / Z;
+  // (a score-ordered row has no finite softmax: its weights and mass are NaN, as torch's are)
   float wv[kSelPer];
   float msum = 0.0f;
 #pragma unroll
@@ -679,19 +775,18 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     const int p = e * kTopkThreads + tid;
     wv[e] = 0.0f;
     if (p < k) {
-      wv[e] = fast_exp2(fmaf(key_value(sh.sel_key[p]), kLog2e, -mlog)) * invZ;
+      wv[e] = weighted ? key_weight(sh.sel_key[p]) : NAN;
       msum += wv[e];
     }
   }
   const float S = res_block_sum(msum, sh);
-  const float invS = 1.0f / S;
 #pragma unroll
   for (int e = 0; e < kSelPer; ++e) {
     const int p = e * kTopkThreads + tid;
     if (p < k) {
       oi[p] = static_cast<int32_t>(sh.sel_idx[p]);
       ov[p] = 1;
-      ow[p] = wv[e] * invS;
+      ow[p] = wv[e] / S;  // selected_global / mass (engine.py:492)
     }
   }
   if (tid == 0) {
@@ -791,9 +886,10 @@ __global__ __launch_bounds__(kTopkThreads) void select_tokens_kernel(const float
     const EligibleCand cand{el, forced ? last : -1};
     uint32_t kth;
     int need;
-    radix_select(x, tokens, remaining, cand, sh, &kth, &need);
+    const auto key_of = [&](int i) { return order_key(x[i]); };
+    radix_select(key_of, tokens, remaining, cand, sh, &kth, &need);
     // positions are written after the forced token is merged in, below
-    selected = compact_selected(x, tokens, kth, need, cand, sh, [&](int i, int) { om[i] = 1; });
+    selected = compact_selected(key_of, tokens, kth, need, cand, sh, [&](int i, int, uint32_t) { om[i] = 1; });
   }
   __threadfence_block();
   __syncthreads();

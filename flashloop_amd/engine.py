@@ -17,7 +17,9 @@ Model GEMMs, norms and SDPA of the dense prefill loops are torch (hipBLASLt).
 
 from __future__ import annotations
 
+import gc
 import math
+import weakref
 from dataclasses import dataclass, field
 from typing import Callable, Sequence
 
@@ -106,11 +108,21 @@ class DecodeRunner:
     not."""
 
     def __init__(self, engine: "FlashLoopEngine", use_graphs: bool) -> None:
-        self.engine = engine
+        # a weak back-reference: the engine and its runner form no cycle, so a dropped
+        # engine frees its graph at once instead of in some later garbage collection,
+        # which may run inside another graph's capture (where destroying a graph aborts)
+        self._engine = weakref.ref(engine)
         self.use_graphs = bool(use_graphs)
         self.graph = None
         self.captures = 0  # graphs captured so far
         self.reset()
+
+    @property
+    def engine(self) -> "FlashLoopEngine":
+        eng = self._engine()
+        if eng is None:
+            raise RuntimeError("the engine of this decode runner no longer exists")
+        return eng
 
     def _release(self) -> None:
         """Destroy the captured graph and its private memory pool, here and now (never
@@ -170,9 +182,19 @@ class DecodeRunner:
                 lc.tail_tokens -= 1
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
-            self.out.copy_(self.logits)
+        # Unreachable objects that own a graph (another engine's, say) must be destroyed
+        # before the capture, not by a collection the capture's allocations trigger: a
+        # graph destroyed while a stream captures aborts the process.
+        gc.collect()
+        was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.graph(graph):
+                self.logits = eng._decode_core(cache, eng.backbone.embed_tokens(self.tok), self.pos)
+                self.out.copy_(self.logits)
+        finally:
+            if was_enabled:
+                gc.enable()
         self.graph = graph
         self.captures += 1
 

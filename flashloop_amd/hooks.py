@@ -251,7 +251,9 @@ def flashloop(model, *, attention_fraction: float = 0.10, fraction_loop3: float 
         if pos is not None and int(torch.as_tensor(pos).flatten()[-1]) != cache.position:
             raise ValueError("flashloop forward: position does not follow the cache")
         out = engine.decode(input_ids)
-        return FlashLoopOutput(out.logits.unsqueeze(1), FlashLoopCache(engine, out.state.next_position))
+        # a copy: the engine's logits buffer is overwritten by the next step's graph replay,
+        # and a caller of an HF-style forward may keep every step's output
+        return FlashLoopOutput(out.logits.unsqueeze(1).clone(), FlashLoopCache(engine, out.state.next_position))
 
     saved = {name: model.__dict__[name] for name in ("generate", "forward") if name in model.__dict__}
     model.generate = generate

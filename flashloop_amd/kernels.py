@@ -171,7 +171,8 @@ def decode_capacity(keys: int, fraction: float) -> int:
 
 def decode_topk(logits: torch.Tensor, n_keys: torch.Tensor, fraction: float, capacity: int,
                 rows_per_count: int = 1, validate: bool = False, nonfinite: torch.Tensor | None = None):
-    """Top-k of each logits row -> (indices i32, valid u8, mass f32, weights f32, counts i32).
+    """Top-k of each logits row by fp32 softmax weight (ties to the lower index) ->
+    (indices i32, valid u8, mass f32, weights f32, counts i32).
 
     ``nonfinite`` (optional i32 [rows]) receives each row's count of NaN/inf scores.
     ``validate=True`` waits for the kernel and raises ``ValueError`` when a row holds one

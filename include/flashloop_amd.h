@@ -207,17 +207,23 @@ int32_t fl_profile_dense_reader_read(float* total_ms, int32_t* launches);
  * -> mass -> normalise of `FlashLoopEngine.decode` (flashloop/engine.py:438-498,
  * 84-109) and `select_decode_keys` (flashloop/selection.py:72-88).  Row r holds
  * n_keys[r / heads_per_count] scores at `scores + r*scores_stride` (the dense reader's
- * logits).  It selects k = min(n, max(1, ceil(n*fraction))) keys, ranked by score,
- * ties to the lower index, and writes them ascending:
+ * logits).  It selects k = min(n, max(1, ceil(n*fraction))) keys ranked by their fp32
+ * softmax weight, as the reference ranks `softmax(logits, dtype=float32)`, ties (equal
+ * fp32 weights, e.g. weights that underflow to 0) to the lower index, and writes them
+ * ascending:
  *   indices i32 [rows, capacity] (0-padded), valid u8 [rows, capacity],
  *   mass f32 [rows] = sum of the selected softmax weights,
  *   weights f32 [rows, capacity] = softmax weight / mass (0 where invalid).
+ * The weight of score x is RN(e * RN(1/Z)) with e = exp(RN(x - max)) from IEEE fma/mul
+ * (within 2 ulp of exp) and Z the sum of e in a fixed order, so it is reproducible
+ * bit for bit off the GPU.
  * `capacity` must be >= k for every row (the engine uses (k/64+1)*64).
  * counts (optional) i32 [rows] receives k.
- * Scores compare as floats: -0.0 and +0.0 are equal (lower index first).
  * nonfinite (optional) i32 [rows] receives the row's number of NaN / +-inf scores;
- * `flashloop/selection.py:78-79` rejects such rows, so a caller that validates checks
- * it (the selection made from a row that holds one is defined but meaningless).
+ * `flashloop/selection.py:78-79` rejects non-finite weights, so a caller that validates
+ * checks it.  A row holding a NaN or +inf (or only -inf) has no finite softmax: its
+ * keys are ranked by score (-0.0 equal to +0.0, -inf as -FLT_MAX, lower index first)
+ * and its mass and weights are NaN, as torch's are.
  */
 int32_t fl_decode_topk(const float* scores, int64_t scores_stride, int32_t rows,
                        const int32_t* n_keys, int32_t rows_per_count, double fraction,

@@ -12,7 +12,8 @@ inputs, the identity ``cached-mass delta == mass_scaled_sparse_output`` of
 flashloop_torch (attention_utils.py:216-248) with ``cached_source_mass`` scales,
 sparse == dense when the fraction is 1 (config.py:73-77), ``sum softmax == 1``,
 ``mass in (0, 1]``, the budget formula, and top-k == a stable argsort on
-``(-score, index)`` / the 3x3 known-answer of attention_utils.py:638-654.
+``(-score, index)`` / the 3x3 known-answer of attention_utils.py:638-654.  The fp32
+softmax weight image the selection ranks is pinned in tests/test_oracle_topk_weights.py.
 """
 
 from __future__ import annotations
@@ -81,20 +82,123 @@ def topk_order(scores: np.ndarray, k: int) -> np.ndarray:
     definition fixes it to the lower index.  A stable argsort on ``-score`` yields
     exactly that order.
     """
-    s = np.asarray(scores, dtype=np.float32)
+    s = np.asarray(scores)
     order = np.argsort(-s.astype(np.float64), kind="stable")
     return np.sort(order[:k]).astype(np.int32)
+
+
+# ---- the fp32 softmax weight image that the decode selection ranks ----------------------
+# engine.py:439-453 (and selection.py:85) rank ``w = softmax(logits, dtype=float32)``: two
+# different logits whose fp32 weights are equal tie, and ties go to the lower index.  The
+# image below is the one the HIP top-k forms, op for op in float32:
+#   e = softmax_exp(RN(x - max)), Z = the sum of e in the kernels' fixed order,
+#   w = RN(e * RN(1 / Z)).
+# Pinned (tests/test_oracle_topk_weights.py) by: fma32 against exact rational arithmetic,
+# softmax_exp within 2 ulp of the float64 exp (and exact at 0 and in the underflow range),
+# Z and w within a few ulp of the float64 softmax, and the ranking equal to torch's own
+# fp32 softmax ranking on rows where the logit ranking differs from it.
+
+_F = np.float32
+LN2_HI = _F(float.fromhex("0x1.62e430p-1"))
+LN2_LO = _F(float.fromhex("-0x1.05c610p-29"))
+INV_LN2 = _F(float.fromhex("0x1.715476p+0"))
+_POLY = [_F(float.fromhex(h)) for h in ("0x1.a01a02p-13", "0x1.6c16c2p-10", "0x1.111112p-7",
+                                         "0x1.555556p-5", "0x1.555556p-3")] + [_F(0.5), _F(1.0), _F(1.0)]
+TOPK_THREADS = 1024
+TOPK_WAVE = 64
+
+
+def fma32(a, b, c) -> np.ndarray:
+    """Correctly rounded float32 ``a*b + c``: the product is exact in float64, the sum is
+    formed in float64 rounded to odd (TwoSum error, then the last bit forced odd when
+    inexact), and one rounding to float32 follows (Boldo & Melquiond, 2008: round-to-odd
+    with >= 2 extra bits makes the double rounding exact)."""
+    a = np.asarray(a, np.float32).astype(np.float64)
+    b = np.asarray(b, np.float32).astype(np.float64)
+    c = np.asarray(c, np.float32).astype(np.float64)
+    p = a * b  # exact: 48 significant bits
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = p + c
+        bb = s - p
+        err = (p - (s - bb)) + (c - bb)
+    bits = s.view(np.int64)
+    fix = (err != 0) & ((bits & 1) == 0) & np.isfinite(s)
+    toward = np.where(err > 0, np.inf, -np.inf)
+    s = np.where(fix, np.nextafter(s, toward), s)
+    return s.astype(np.float32)
+
+
+def softmax_exp32(d) -> np.ndarray:
+    """The kernels' fp32 ``exp(d)`` for ``d <= 0`` (topk.hip ``softmax_exp``): Cody-Waite
+    reduction with ``n = rint(d / ln2)``, degree-7 Taylor polynomial by Horner in fma, and
+    the scale ``2^n`` as an exact multiply by ``2^(n+64)`` then a rounding multiply by
+    ``2^-64``."""
+    d = np.maximum(np.asarray(d, np.float32), _F(-112.0))
+    n = np.rint(d * INV_LN2)
+    r = fma32(n, -LN2_HI, d)
+    r = fma32(n, -LN2_LO, r)
+    p = np.full_like(r, _POLY[0])
+    for c in _POLY[1:]:
+        p = fma32(p, r, c)
+    up = ((n.astype(np.int32) + 64 + 127) << 23).astype(np.uint32).view(np.float32)
+    return (p * up) * _F(2.0 ** -64)
+
+
+def weight_sum_fixed(e: np.ndarray) -> np.float32:
+    """The kernels' normaliser: thread t of 1024 sums indices t, t+1024, ... in order; each
+    wave of 64 threads adds lane pairs at distance 32, 16, ..., 1; the 16 wave sums are
+    added in wave order."""
+    e = np.asarray(e, np.float32)
+    n = e.shape[0]
+    rows = max(1, -(-n // TOPK_THREADS))
+    buf = np.zeros(rows * TOPK_THREADS, np.float32)
+    buf[:n] = e
+    buf = buf.reshape(rows, TOPK_THREADS)
+    z = buf[0].copy()
+    for j in range(1, rows):
+        z = z + buf[j]
+    v = z.reshape(TOPK_THREADS // TOPK_WAVE, TOPK_WAVE)
+    lanes = np.arange(TOPK_WAVE)
+    off = TOPK_WAVE // 2
+    while off >= 1:
+        v = v + v[:, lanes ^ off]
+        off //= 2
+    total = v[0, 0]
+    for w in range(1, v.shape[0]):
+        total = np.float32(total + v[w, 0])
+    return np.float32(total)
+
+
+def weight_image(x) -> np.ndarray | None:
+    """fp32 softmax weights of one logits row as the top-k ranks them, or ``None`` when the
+    row holds a NaN or +inf (or only -inf): torch's fp32 softmax is NaN throughout then,
+    and the kernels rank the scores themselves (ties to the lower index, -inf as -FLT_MAX)."""
+    x = np.asarray(x, np.float32)
+    if x.size == 0 or np.isnan(x).any() or np.isposinf(x).any() or not np.isfinite(x.max()):
+        return None
+    m = x.max()
+    e = softmax_exp32(x - m)
+    inv = np.float32(np.float32(1.0) / weight_sum_fixed(e))
+    return e * inv
+
+
+def score_order_key(x) -> np.ndarray:
+    """Ranking key of a row without finite weights (topk.hip ``score_key``): the float's
+    order-preserving unsigned image (``-0.0`` folded into ``+0.0`` by adding ``+0.0``;
+    NaN keeps its sign), floored at the image of ``-FLT_MAX``."""
+    u = (np.asarray(x, np.float32) + np.float32(0.0)).view(np.uint32)
+    key = np.where((u & np.uint32(0x80000000)) != 0, ~u, u | np.uint32(0x80000000))
+    return np.maximum(key, np.uint32(0x00800000))
 
 
 def decode_topk(logits, fraction: float, kpad: int | None = None) -> DecodeSelection:
     """Loop-2 key selection of ``FlashLoopEngine.decode`` (engine.py:438-498).
 
-    ``w = softmax_fp32(logits)``; ``k = budget``; top-k -> ascending sort -> pad to a
-    64 multiple with a validity mask; ``mass = sum w_S``; ``selected_weights = w / mass``.
-    The ranking key is the fp32 logit itself (the strictly monotone pre-image of ``w``);
-    it equals ranking ``w`` except where fp32 rounding makes two different logits produce
-    the same ``w`` (``tests/test_oracle_attention.py`` counts such ties on the fixtures).
-    ``logits``: ``[R, N]`` array or a list of 1-D arrays (ragged rows).
+    ``w = softmax_fp32(logits)`` (the image of ``weight_image``); ``k = budget``; top-k of
+    ``w`` with ties to the lower index -> ascending sort -> pad to a 64 multiple with a
+    validity mask; ``mass = sum w_S``; ``selected_weights = w_S / mass``.  A row without
+    finite weights (``weight_image`` is ``None``) is ranked by its scores and gets NaN
+    mass and weights.  ``logits``: ``[R, N]`` array or a list of 1-D arrays (ragged rows).
     """
     rows = [np.asarray(x, dtype=np.float32) for x in logits]
     counts = [decode_budget(len(x), fraction) for x in rows]
@@ -107,12 +211,17 @@ def decode_topk(logits, fraction: float, kpad: int | None = None) -> DecodeSelec
     sw = np.zeros((R, kpad), np.float64)
     for r, x in enumerate(rows):
         k = counts[r]
-        sel = topk_order(x, k)
-        w = _softmax64(x.astype(np.float64))
+        w = weight_image(x)
+        if w is None:
+            sel = topk_order(score_order_key(x).astype(np.int64), k)
+            mass[r] = np.nan
+            sw[r, :k] = np.nan
+        else:
+            sel = topk_order(w, k)
+            mass[r] = w[sel].astype(np.float64).sum()
+            sw[r, :k] = w[sel] / mass[r]
         idx[r, :k] = sel
         valid[r, :k] = True
-        mass[r] = w[sel].sum()
-        sw[r, :k] = w[sel] / mass[r]
     return DecodeSelection(idx, valid, mass, sw, np.asarray(counts))
 
 

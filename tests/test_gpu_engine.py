@@ -286,11 +286,17 @@ def test_hooks_route_forward_and_generate_with_observed_counters(tmp_path):
         assert torch.equal(torch.argmax(out.logits[:, -1], -1), torch.argmax(ref_pre.logits, -1))
         cache = out.past_key_values
         tok = torch.argmax(out.logits[:, -1], dim=-1, keepdim=True)
+        kept = []
         for i in range(steps):
             o = model(tok, past_key_values=cache)
             assert torch.equal(o.logits[:, 0], ref_steps[i]), f"routed decode step {i}"
+            kept.append(o.logits)  # held as an HF caller holds them (graph replays follow)
             cache = o.past_key_values
             tok = torch.argmax(o.logits[:, 0], dim=-1, keepdim=True)
+        # every kept step still holds its own logits after the later replays
+        for i, lg in enumerate(kept):
+            assert torch.equal(lg[:, 0], ref_steps[i]), f"kept logits of step {i} were overwritten"
+        assert not torch.equal(kept[0], kept[-1])
         with pytest.raises(ValueError):
             model(tok, past_key_values=out.past_key_values)  # stale
         kv = hooks["kv"].audit()

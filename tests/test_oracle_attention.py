@@ -65,7 +65,7 @@ def test_decode_topk_mass_and_weights():
         k = sel.count[r]
         assert np.all(np.diff(sel.indices[r, :k]) > 0)
         assert np.all(sel.indices[r, k:] == 0) and not sel.valid[r, k:].any()
-        assert abs(sel.mass[r] - w[sel.indices[r, :k]].sum()) < 1e-12
+        assert abs(sel.mass[r] - w[sel.indices[r, :k]].sum()) < 1e-6  # fp32 weight image
         assert 0 < sel.mass[r] <= 1
         assert abs(sel.selected_weights[r].sum() - 1) < 1e-12
         # the selected set is the k largest weights
