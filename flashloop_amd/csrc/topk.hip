@@ -22,6 +22,9 @@ namespace {
 
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / kWave;
+// Slot order of a row's keys over a workgroup: key q*4096 + 4t + e is thread t's slot
+// 4q + e, so a thread reads 16 contiguous bytes per quad chunk q.
+constexpr int kQuadChunk = 4 * kTopkThreads;
 
 // Order-preserving unsigned key of a score.  -0.0 takes the key of +0.0 (they compare
 // equal, so the lower index wins their tie, as in torch.topk and a stable sort): adding
@@ -286,11 +289,14 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
   __syncthreads();
   if (threadIdx.x == 0) sh.nonfin &= 0x3FFFFFFFu;
   // the same weight image and summation order as the register-resident kernel: thread t
-  // sums indices t, t + 1024, ... in order, then the fixed-order block sum
+  // sums indices q*4096 + 4t + e in (q, e) order, then the fixed-order block sum
   float invZ = 0.0f;
   if (weighted) {
     float z = 0.0f;
-    for (int i = threadIdx.x; i < n; i += kTopkThreads) z += softmax_exp(x[i] - M);
+    for (int base = 4 * threadIdx.x; base < n; base += kQuadChunk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (base + e < n) z += softmax_exp(x[base + e] - M);
     invZ = 1.0f / res_block_sum_fixed(z, sh);
   }
   const auto key_of = [&](int i) {
@@ -328,22 +334,24 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
 }
 
 // Register-resident variant for rows of at most kResKeys keys and k <= kSelLds: thread t
-// holds keys t, t + 1024, t + 2048, ... in registers for the whole kernel, so no pass
+// holds keys q*4096 + 4t + e (slot 4q + e) in registers for the whole kernel, so no pass
 // after the load re-reads the row.  The passes are VALU-bound (one row per CU), so each
 // is kept to a few instructions per key:
-//   1. load as order-preserving keys (all loads issued first), row max and min;
-//   2. softmax normaliser and a histogram over kBins value-linear bins -- the bin is a
-//      non-decreasing function of the score, so the k-th largest key lies in the bin B*
-//      where the count from the top reaches k, and every key of a higher bin is larger;
-//   3. per (chunk, wave) ballot counts of the keys above B*, and the keys of B* (a few
-//      dozen for smooth score distributions) compacted into an LDS list, ranked there by
-//      (score desc, index asc): that fixes the k-th key (kth_key, kth_idx) and adds the
+//   1. load (one dwordx4 per quad, all issued first), row max and min;
+//   2. the keys: the fp32 softmax weight image (or the score order in a row without
+//      finite weights);
+//   3. a histogram over kBins key-linear bins -- the bin is a non-decreasing function of
+//      the key, so the k-th largest key lies in the bin B* where the count from the top
+//      reaches k, and every key of a higher bin is larger;
+//   4. per (quad chunk, wave) ballot counts of the keys above B*, and the keys of B* (a
+//      few dozen for smooth score distributions) compacted into an LDS list, ranked there
+//      by (key desc, index asc): that fixes the k-th key (kth_key, kth_idx) and adds the
 //      selected keys of B* to their (chunk, wave) counts -- a bin too crowded for the
 //      list falls back to an exact radix select restricted to B* and a counting pass;
-//   4. one prefix scan of the counts, then each lane stores its selected (index, key) at
+//   5. one prefix scan of the counts, then each lane stores its selected (index, key) at
 //      its offset in an LDS list, which is therefore in index order;
-//   5. the k list entries get their softmax weights and are written out coalesced.
-constexpr int kPer = 35;  // most keys per thread (rows of up to kResKeys keys)
+//   6. the k list entries get their softmax weights and are written out coalesced.
+constexpr int kPer = 36;  // most keys per thread (rows of up to kResKeys keys); a multiple of 4
 constexpr int kResKeys = kPer * kTopkThreads;
 constexpr int kSelLds = 8 * kTopkThreads;  // selected-list capacity of the resident kernel
 constexpr int kSelPer = kSelLds / kTopkThreads;
@@ -351,13 +359,6 @@ constexpr int kSubHist = 4;
 constexpr int kBins = kSubHist * 256;  // value-linear bins of the boundary search (one per thread)
 constexpr int kCand = 512;             // boundary-bin list capacity
 static_assert(kBins == kTopkThreads, "one boundary bin per thread");
-
-// Non-decreasing in x (fma rounding is monotone for inv >= 0); NaN and negative products
-// fall in bin 0, so the index is always in range.  Every pass uses this one function.
-__device__ __forceinline__ int value_bin(float x, float inv, float off) {
-  const float b = fminf(fmaxf(fmaf(x, inv, off), 0.0f), static_cast<float>(kBins - 1));
-  return static_cast<int>(b);
-}
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
@@ -475,11 +476,15 @@ struct TopkArgs {
   int32_t* nonfinite;
 };
 
-// Top-k of row r = blockIdx.x (key_count(r) keys) by one 1024-thread workgroup.
+// Top-k of row r = blockIdx.x (key_count(r) keys) by one 1024-thread workgroup.  Slot
+// j = 4q + e of thread t holds key q*4096 + 4t + e: each thread loads 16 bytes per quad
+// chunk (one dwordx4 load per 4 keys; dword loads had made the load pass 4x longer).
 template <int PER, typename KeyCount>
 __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_count, const float* scores, int64_t stride,
                                                   double fraction, int cap, int32_t* indices, uint8_t* valid,
                                                   float* mass, float* weights, int32_t* counts, int32_t* nonfinite) {
+  static_assert(PER % 4 == 0 && PER <= kPer, "keys per thread: whole quads within the LDS arrays");
+  constexpr int Q = PER / 4;
   const int r = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -510,23 +515,51 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     }
     return;
   }
+  const auto index_of = [&](int j) { return (j >> 2) * kQuadChunk + 4 * tid + (j & 3); };
 
-  // ---- 1. load (slot j of thread t is index j * 1024 + t), row max and min, and what
-  // kinds of non-finite score the row holds (the max of |x|'s bits: > inf's bits is NaN)
+  // ---- 1. load, row max and min, and what kinds of non-finite score the row holds (the
+  // max of |x|'s bits: above inf's bits is a NaN).  Every load is issued before the first
+  // use: bounds-checked buffer loads (keys past n read as zero, then replaced by -inf),
+  // 16 bytes per quad when the row is 16-byte aligned; the one lane whose quad straddles
+  // n reloads its keys.
   uint32_t kr[PER];  // the score bits, then e's bits, then the ranking key (0 = padding)
   float mx = -INFINITY, mn = INFINITY;
   uint32_t amax = 0;
   if (tid == 0) sh.nonfin = 0;
   {
+    const __amdgpu_buffer_rsrc_t res =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0, n * static_cast<int>(sizeof(float)), 0x00020000);
     float xs[PER];
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) {  // (row-uniform) 16-byte aligned row
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = j * kTopkThreads + tid;
-      xs[j] = (i < n) ? x[i] : -INFINITY;
+      for (int q = 0; q < Q; ++q) {
+        const float4 t4 = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(res, (q * kQuadChunk + 4 * tid) * 4, 0, 0));
+        xs[4 * q] = t4.x;
+        xs[4 * q + 1] = t4.y;
+        xs[4 * q + 2] = t4.z;
+        xs[4 * q + 3] = t4.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        xs[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, index_of(j) * 4, 0, 0));
+    }
+    const int qs = (n - 1) / kQuadChunk, ts = ((n - 1) % kQuadChunk) >> 2;  // the straddling quad
+    if ((n & 3) != 0 && tid == ts) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+        if (q == qs)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = q * kQuadChunk + 4 * tid + e;
+            if (i < n) xs[4 * q + e] = x[i];
+          }
     }
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const bool in = j * kTopkThreads + tid < n;
+      const bool in = index_of(j) < n;
+      xs[j] = in ? xs[j] : -INFINITY;
       kr[j] = __float_as_uint(xs[j]);
       amax = max(amax, in ? kr[j] & 0x7FFFFFFFu : 0u);
       mx = fmaxf(mx, xs[j]);
@@ -545,7 +578,8 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
   const bool weighted = ext.z < 2.0f && M > -INFINITY && M < INFINITY;
   const bool badrow = ext.z != 0.0f;  // some score may be non-finite: counted below
 
-  // ---- 2. the weight image (weighted rows) or the score order, as keys
+  // ---- 2. the weight image (weighted rows) or the score order, as keys.  Thread t sums
+  // its e in slot order, then the fixed-order block sum.
   float invZ = 0.0f;
   uint32_t kmin = kScoreKeyFloor, shift = 31u, binmax = 0u;  // a score-ordered row: one bin
   if (weighted) {
@@ -559,7 +593,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     const float Z = res_block_sum_fixed(z, sh);
     invZ = 1.0f / Z;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) kr[j] = (j * kTopkThreads + tid < n) ? weight_key(__uint_as_float(kr[j]), invZ) : 0u;
+    for (int j = 0; j < PER; ++j) kr[j] = index_of(j) < n ? weight_key(__uint_as_float(kr[j]), invZ) : 0u;
     // keys lie in [key(min score), key(max score) = bits(invZ) + 1]; bins of 2^shift keys
     kmin = weight_key(softmax_exp(mn - M), invZ);
     const uint32_t span = max(__float_as_uint(invZ) + 1u, kmin) - kmin;
@@ -567,10 +601,10 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     binmax = kBins - 1;
   } else {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) kr[j] = (j * kTopkThreads + tid < n) ? score_key(__uint_as_float(kr[j])) : 0u;
+    for (int j = 0; j < PER; ++j) kr[j] = index_of(j) < n ? score_key(__uint_as_float(kr[j])) : 0u;
   }
 
-  // ---- 3. value histogram: bin(key) is non-decreasing in the key (and 0 for padding)
+  // ---- 3. histogram: bin(key) is non-decreasing in the key (and 0 for padding)
   uint32_t* lin = &sh.hist[0][0];  // one kBins-bin histogram (the sub-histograms are for the radix)
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -609,33 +643,41 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
   const int bstar = static_cast<int>(sh.sel_digit);
   const int need_b = k - static_cast<int>(sh.bin_above);  // >= 1 keys of B* are selected
 
-  // ---- 3. counts of the keys above B*; keys of B* -> LDS list (one LDS atomic per wave)
-  uint32_t cnt_lane = 0;  // lane j: this wave's count of chunk j
+  // ---- 4. counts of the keys above B* per (quad chunk, wave); keys of B* -> LDS list
+  // (one LDS atomic per wave)
+  uint32_t cnt_lane = 0;  // lane q: this wave's count of quad chunk q
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = j * kTopkThreads + tid;
-    const int b = sh.bin[j][tid];
-    const uint64_t bal_a = ballot64(b > bstar);
-    const bool in_b = b == bstar && kr[j] != 0u;
-    const uint64_t bal_b = ballot64(in_b);
-    cnt_lane = lane == j ? static_cast<uint32_t>(__popcll(bal_a)) : cnt_lane;
-    if (bal_b != 0ull) {
-      uint32_t base = 0;
-      if (lane == 0) base = atomicAdd(&sh.ncand, static_cast<uint32_t>(__popcll(bal_b)));
-      base = __shfl(base, 0, kWave);
-      const uint32_t slot = base + static_cast<uint32_t>(__popcll(bal_b & lt_mask));
-      if (in_b && slot < kCand) {
-        sh.cand_key[slot] = kr[j];
-        sh.cand_idx[slot] = static_cast<uint32_t>(i);
+  for (int q = 0; q < Q; ++q) {
+    uint32_t c = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = 4 * q + e;
+      const int b = sh.bin[j][tid];
+      c += static_cast<uint32_t>(__popcll(ballot64(b > bstar)));
+      const bool in_b = b == bstar && kr[j] != 0u;
+      const uint64_t bal_b = ballot64(in_b);
+      if (bal_b != 0ull) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&sh.ncand, static_cast<uint32_t>(__popcll(bal_b)));
+        base = __shfl(base, 0, kWave);
+        const uint32_t slot = base + static_cast<uint32_t>(__popcll(bal_b & lt_mask));
+        if (in_b && slot < kCand) {
+          sh.cand_key[slot] = kr[j];
+          sh.cand_idx[slot] = static_cast<uint32_t>(index_of(j));
+        }
       }
     }
+    cnt_lane = lane == q ? c : cnt_lane;
   }
-  if (lane < PER) sh.cnt[lane][w] = cnt_lane;
+  if (lane < Q) sh.cnt[lane][w] = cnt_lane;
   if (tid < kCand) sh.cand_rank[tid] = 0;
   __syncthreads();
+  // (quad chunk, wave) of key index i
+  const auto chunk_of = [](uint32_t i) { return i / kQuadChunk; };
+  const auto wave_of = [](uint32_t i) { return ((i % kQuadChunk) >> 2) / kWave; };
   const int m = static_cast<int>(sh.ncand);
   if (m <= kCand) {
-    // rank of each candidate = how many candidates precede it in (score desc, index asc)
+    // rank of each candidate = how many candidates precede it in (key desc, index asc)
     // order.  The m x m comparisons are spread over all waves: wave w compares the 64
     // candidates of block w % nb against slice w / nb of the list.
     const int nb = (m + kWave - 1) / kWave;  // <= 8
@@ -659,7 +701,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     if (tid < m) {
       const uint32_t mi = sh.cand_idx[tid];
       const int rank = static_cast<int>(sh.cand_rank[tid]);
-      if (rank < need_b) atomicAdd(&sh.cnt[mi / kTopkThreads][(mi % kTopkThreads) / kWave], 1u);
+      if (rank < need_b) atomicAdd(&sh.cnt[chunk_of(mi)][wave_of(mi)], 1u);
       if (rank == need_b - 1) {
         sh.kth_key = sh.cand_key[tid];
         sh.kth_idx = mi;
@@ -667,18 +709,18 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     }
     __syncthreads();
   } else {
-    // crowded bin (many equal or clustered scores): exact radix select within B*
+    // crowded bin (many equal or clustered keys): exact radix select within B*
     uint32_t prefix = 0, pmask = 0;
     int remaining = need_b;
     uint32_t* hist = &sh.hist[w & (kSubHist - 1)][0];
-    for (int shift = 24; shift >= 0; shift -= 8) {
+    for (int shift8 = 24; shift8 >= 0; shift8 -= 8) {
       for (int i = tid; i < kSubHist * 256; i += kTopkThreads) (&sh.hist[0][0])[i] = 0;
       __syncthreads();
 #pragma unroll
       for (int j = 0; j < PER; ++j) {
         const uint32_t kk = kr[j];
         if (kk != 0u && (kk & pmask) == prefix && static_cast<int>(sh.bin[j][tid]) == bstar)
-          atomicAdd(&hist[(kk >> shift) & 0xFFu], 1u);
+          atomicAdd(&hist[(kk >> shift8) & 0xFFu], 1u);
       }
       __syncthreads();
       if (tid < kWave) {
@@ -689,7 +731,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
           const int bin = 255 - 4 * lane - e;
           h[e] = 0;
 #pragma unroll
-          for (int q = 0; q < kSubHist; ++q) h[e] += sh.hist[q][bin];
+          for (int qh = 0; qh < kSubHist; ++qh) h[e] += sh.hist[qh][bin];
           local += h[e];
         }
         uint32_t incl = local;
@@ -709,64 +751,89 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
         }
       }
       __syncthreads();
-      prefix |= sh.sel_digit << shift;
-      pmask |= 0xFFu << shift;
+      prefix |= sh.sel_digit << shift8;
+      pmask |= 0xFFu << shift8;
       remaining -= static_cast<int>(sh.bin_above);
       __syncthreads();
     }
     // the `remaining`-th key equal to `prefix` in index order is the k-th key
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const bool eq = kr[j] == prefix;
-      const uint64_t bal = ballot64(eq);
-      if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
+    for (int q = 0; q < Q; ++q) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c += static_cast<uint32_t>(__popcll(ballot64(kr[4 * q + e] == prefix)));
+      if (lane == 0) sh.cnt[q][w] = c;
     }
     __syncthreads();
-    prefix_counts<PER>(sh);
+    prefix_counts<Q>(sh);
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = j * kTopkThreads + tid;
-      const bool eq = kr[j] == prefix;
-      const uint64_t bal = ballot64(eq);
-      const int rank = static_cast<int>(sh.cnt[j][w]) + __popcll(bal & lt_mask);
-      if (eq && rank == remaining - 1) {
-        sh.kth_key = prefix;
-        sh.kth_idx = static_cast<uint32_t>(i);
+    for (int q = 0; q < Q; ++q) {
+      uint64_t bal[4];
+      uint32_t before = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bal[e] = ballot64(kr[4 * q + e] == prefix);
+        before += static_cast<uint32_t>(__popcll(bal[e] & lt_mask));
+      }
+      int rank = static_cast<int>(sh.cnt[q][w] + before);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (kr[4 * q + e] == prefix) {
+          if (rank == remaining - 1) {
+            sh.kth_key = prefix;
+            sh.kth_idx = static_cast<uint32_t>(index_of(4 * q + e));
+          }
+          ++rank;
+        }
       }
     }
     __syncthreads();
     const uint32_t kk0 = sh.kth_key, ki0 = sh.kth_idx;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = j * kTopkThreads + tid;
-      const uint32_t kk = kr[j];
-      const bool sel = kk > kk0 || (kk == kk0 && static_cast<uint32_t>(i) <= ki0);
-      const uint64_t bal = ballot64(sel);
-      if (lane == 0) sh.cnt[j][w] = static_cast<uint32_t>(__popcll(bal));
+    for (int q = 0; q < Q; ++q) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t kk = kr[4 * q + e];
+        const bool sel = kk > kk0 || (kk == kk0 && static_cast<uint32_t>(index_of(4 * q + e)) <= ki0);
+        c += static_cast<uint32_t>(__popcll(ballot64(sel)));
+      }
+      if (lane == 0) sh.cnt[q][w] = c;
     }
     __syncthreads();
   }
   const uint32_t kth_key = sh.kth_key;
   const uint32_t kth_idx = sh.kth_idx;
-  prefix_counts<PER>(sh);  // (its barrier also publishes the counts to every wave)
+  prefix_counts<Q>(sh);  // (its barrier also publishes the counts to every wave)
 
-  // ---- 4. selected (index, key) pairs into the LDS list, in index order
-  const uint32_t base_lane = lane < PER ? sh.cnt[lane][w] : 0u;  // lane j: offset of chunk j
+  // ---- 5. selected (index, key) pairs into the LDS list, in index order: the offset of
+  // (chunk q, wave w), then the selected keys of the lower lanes, then this lane's own
+  const uint32_t base_lane = lane < Q ? sh.cnt[lane][w] : 0u;  // lane q: offset of chunk q
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = j * kTopkThreads + tid;
-    const uint32_t kk = kr[j];
-    const bool sel = kk > kth_key || (kk == kth_key && static_cast<uint32_t>(i) <= kth_idx);
-    const uint64_t bal = ballot64(sel);
-    const int pos = static_cast<int>(__builtin_amdgcn_readlane(base_lane, j)) + __popcll(bal & lt_mask);
-    if (sel && pos < k) {
-      sh.sel_idx[pos] = static_cast<uint32_t>(i);
-      sh.sel_key[pos] = kk;
+  for (int q = 0; q < Q; ++q) {
+    bool sel[4];
+    uint32_t before = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t kk = kr[4 * q + e];
+      sel[e] = kk > kth_key || (kk == kth_key && static_cast<uint32_t>(index_of(4 * q + e)) <= kth_idx);
+      before += static_cast<uint32_t>(__popcll(ballot64(sel[e]) & lt_mask));
+    }
+    int pos = static_cast<int>(__builtin_amdgcn_readlane(base_lane, q) + before);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (sel[e]) {
+        if (pos < k) {
+          sh.sel_idx[pos] = static_cast<uint32_t>(index_of(4 * q + e));
+          sh.sel_key[pos] = kr[4 * q + e];
+        }
+        ++pos;
+      }
     }
   }
   __syncthreads();
 
-  // ---- 5. weights of the k selected keys, coalesced output
+  // ---- 6. weights of the k selected keys, coalesced output
   // (a score-ordered row has no finite softmax: its weights and mass are NaN, as torch's are)
   float wv[kSelPer];
   float msum = 0.0f;
@@ -937,10 +1004,10 @@ int32_t launch_select_merge(const fl_cache_view& v, const float* ws, int W, floa
   const int rows = v.batch * v.heads;
   const int per = static_cast<int>((logits_stride + kTopkThreads - 1) / kTopkThreads);
   const dim3 grid(2 * rows), block(kTopkThreads);
-  if (per <= 9)
-    hipLaunchKernelGGL(select_merge_kernel<9>, grid, block, 0, st, A, v, ws, W, out);
-  else if (per <= 18)
-    hipLaunchKernelGGL(select_merge_kernel<18>, grid, block, 0, st, A, v, ws, W, out);
+  if (per <= 12)
+    hipLaunchKernelGGL(select_merge_kernel<12>, grid, block, 0, st, A, v, ws, W, out);
+  else if (per <= 20)
+    hipLaunchKernelGGL(select_merge_kernel<20>, grid, block, 0, st, A, v, ws, W, out);
   else
     hipLaunchKernelGGL(select_merge_kernel<kPer>, grid, block, 0, st, A, v, ws, W, out);
   FL_LAUNCH_CHECK("fl_decode_attn_dense_select(select+merge)");
@@ -970,11 +1037,11 @@ extern "C" int32_t fl_decode_topk(const float* scores, int64_t scores_stride, in
   // keys per thread: the smallest instantiation that holds the row stride
   const int per = static_cast<int>((scores_stride + kTopkThreads - 1) / kTopkThreads);
   if (scores_stride <= kResKeys && std::ceil(static_cast<double>(scores_stride) * fraction) <= kSelLds) {
-    if (per <= 9)
-      hipLaunchKernelGGL(decode_topk_resident_kernel<9>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+    if (per <= 12)
+      hipLaunchKernelGGL(decode_topk_resident_kernel<12>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
                        fraction, capacity, indices, valid, mass, weights, counts, nonfinite);
-    else if (per <= 18)
-      hipLaunchKernelGGL(decode_topk_resident_kernel<18>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
+    else if (per <= 20)
+      hipLaunchKernelGGL(decode_topk_resident_kernel<20>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,
                        fraction, capacity, indices, valid, mass, weights, counts, nonfinite);
     else
       hipLaunchKernelGGL(decode_topk_resident_kernel<kPer>, grid, block, 0, st, scores, scores_stride, n_keys, rows_per_count,

@@ -145,18 +145,21 @@ def softmax_exp32(d) -> np.ndarray:
 
 
 def weight_sum_fixed(e: np.ndarray) -> np.float32:
-    """The kernels' normaliser: thread t of 1024 sums indices t, t+1024, ... in order; each
-    wave of 64 threads adds lane pairs at distance 32, 16, ..., 1; the 16 wave sums are
-    added in wave order."""
+    """The kernels' normaliser: thread t of 1024 sums indices q*4096 + 4t + e in (q, e)
+    order (4 contiguous keys per thread per 4096-key chunk); each wave of 64 threads adds
+    lane pairs at distance 32, 16, ..., 1; the 16 wave sums are added in wave order."""
     e = np.asarray(e, np.float32)
     n = e.shape[0]
-    rows = max(1, -(-n // TOPK_THREADS))
-    buf = np.zeros(rows * TOPK_THREADS, np.float32)
+    chunk = 4 * TOPK_THREADS
+    rows = max(1, -(-n // chunk))
+    buf = np.zeros(rows * chunk, np.float32)
     buf[:n] = e
-    buf = buf.reshape(rows, TOPK_THREADS)
-    z = buf[0].copy()
-    for j in range(1, rows):
-        z = z + buf[j]
+    buf = buf.reshape(rows, TOPK_THREADS, 4)
+    z = buf[0, :, 0].copy()
+    for q in range(rows):
+        for j in range(4):
+            if q or j:
+                z = z + buf[q, :, j]
     v = z.reshape(TOPK_THREADS // TOPK_WAVE, TOPK_WAVE)
     lanes = np.arange(TOPK_WAVE)
     off = TOPK_WAVE // 2

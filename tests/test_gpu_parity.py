@@ -261,12 +261,15 @@ def test_topk_ranks_fp32_softmax_weights(n):
     assert d_logit >= rows // 3 - 1  # the peaked rows (but the last): the logit order is not the reference's
 
 
-def test_topk_ragged_rows_and_budget_edges():
-    print("case: topk ragged", flush=True)
+@pytest.mark.parametrize("width", [5000, 4999])
+def test_topk_ragged_rows_and_budget_edges(width):
+    """Key counts that end mid-quad (one lane of the row's last 4-key quad reloads its keys)
+    and, with width 4999, rows that start off the 16-byte alignment of a 4-key load."""
+    print("case: topk ragged width=%d" % width, flush=True)
     rng = np.random.default_rng(4)
-    n_keys = [1, 7, 64, 640, 641, 5000]
+    n_keys = [1, 7, 64, 640, 641, 4097, width]
     rows = len(n_keys)
-    lg = rng.standard_normal((rows, 5000)).astype(np.float32) * 3
+    lg = rng.standard_normal((rows, width)).astype(np.float32) * 3
     frac = 0.1
     cap = max(OA.padded_capacity(OA.decode_budget(n, frac)) for n in n_keys)
     t = torch.from_numpy(lg).to(DEV)

@@ -88,15 +88,16 @@ def test_softmax_exp_accuracy_and_special_values():
 def test_weight_sum_order_is_the_kernels():
     """The vectorised fixed-order sum equals the literal per-thread / per-wave loops."""
     rng = np.random.default_rng(2)
-    for n in (1, 63, 1024, 3000, 5000):
+    for n in (1, 63, 1024, 3000, 5000, 9001):
         e = (rng.random(n) * 3).astype(np.float32)
         threads = [np.float32(0.0)] * 1024
         for t in range(1024):
             acc = np.float32(0.0)
-            i = t
-            while i < n:
-                acc = np.float32(acc + e[i])
-                i += 1024
+            base = 4 * t
+            while base < n:
+                for i in range(base, min(base + 4, n)):
+                    acc = np.float32(acc + e[i])
+                base += 4096
             threads[t] = acc
         waves = []
         for w in range(16):
