@@ -5,6 +5,7 @@ from __future__ import annotations
 import numpy as np
 import torch
 
+from oracle import attention as OA
 from oracle import codec
 
 
@@ -30,9 +31,11 @@ def oracle_prefix(keys, values, m3=None, m4=None):
     return nk, nv, chain, tp
 
 
-def assert_layer_matches_chain(layer, chain, tp, batch, heads):
-    """Bit-exact codes, K/V metadata of all four streams against the oracle chain."""
+def assert_layer_matches_chain(layer, chain, tp, batch, heads, row_ids=None):
+    """Bit-exact codes, K/V metadata of all four streams against the oracle chain.
+    ``row_ids``: the layer's (b,h) rows of the chain's rows (default: the same rows)."""
     bh = batch * heads
+    ids = np.arange(bh) if row_ids is None else np.asarray(row_ids)
     G = tp // 64
     for s in range(4):
         sc = chain.streams[s]
@@ -42,8 +45,8 @@ def assert_layer_matches_chain(layer, chain, tp, batch, heads):
         vmeta = layer.value_meta[s].cpu().numpy()
         ks = sc.k_scale.reshape(bh, G, 128)
         km = sc.k_min.reshape(bh, G, 128)
-        assert np.array_equal(kmeta[:, :G, :, 0], ks), f"stream {s}: K scale mismatch"
-        assert np.array_equal(kmeta[:, :G, :, 1], km), f"stream {s}: K min mismatch"
+        assert np.array_equal(kmeta[ids, :G, :, 0], ks), f"stream {s}: K scale mismatch"
+        assert np.array_equal(kmeta[ids, :G, :, 1], km), f"stream {s}: K min mismatch"
         okc = sc.k_codes.reshape(batch, heads, tp, 128)
         ovc = sc.v_codes.reshape(batch, heads, tp, 128)
         ovs = sc.v_scale.reshape(batch, heads, tp, 2)
@@ -59,7 +62,7 @@ def assert_layer_matches_chain(layer, chain, tp, batch, heads):
                 assert np.all(rows >= 0), "active row without a rank"
                 assert np.all(rank[:tp][~act] == -1)
             for h in range(heads):
-                r = b * heads + h
+                r = ids[b * heads + h]
                 assert np.array_equal(kc[r, rows], okc[b, h, t_idx]), f"stream {s}: K codes mismatch (b={b}, h={h})"
                 assert np.array_equal(vc[r, rows], ovc[b, h, t_idx]), f"stream {s}: V codes mismatch (b={b}, h={h})"
                 assert np.array_equal(vmeta[r, rows, :, 0], ovs[b, h, t_idx]), f"stream {s}: V scale mismatch"
@@ -128,3 +131,35 @@ def restated_dense_logits(layer, loop: int, rows, q, k_cur, scaling: float) -> l
         lg[tp + tl] = np.asarray(k_cur[i], np.float64) @ qd
         out.append(lg)
     return out
+
+
+def step_vs_oracle_rows(got, rows, H, nk, nv, masks, q, kc, vc, scaling, fraction, what=""):
+    """One decode step of a batch-one cache against the oracle at the head rows ``rows``.
+
+    ``got``: the step's tensors (``out0``, ``out1`` [H,128]-shaped, ``logits1`` [H, >= T+1],
+    ``indices`` [H, cap], ``delta2``, ``delta3``); ``nk``/``nv``: per loop, float32
+    ``[1, len(rows), T, 128]`` K/V of every cached token of those heads; ``masks``: the
+    loop-3/4 active rows ``(m3, m4)`` ``[1, T]`` or None; ``q``/``kc``/``vc``: per loop,
+    ``[len(rows), 128]``.  Checks the loop-1/2 outputs, the selection bit for bit on the
+    kernel's logits and the loop-3/4 deltas.  Returns the oracle chain and its prefix."""
+    chain, tp = codec.compress_prefix(nk, nv, masks)
+    K, V = materialized(nk, nv, chain, tp)
+    T = nk[0].shape[2]
+    idx = np.asarray(rows)
+    Kr = [flat_rows(K[r]) for r in range(4)]
+    Vr = [flat_rows(V[r]) for r in range(4)]
+    o0, _ = OA.dense_decode(q[0], Kr[0], Vr[0], kc[0], vc[0], scaling)
+    o1, _ = OA.dense_decode(q[1], Kr[1], Vr[1], kc[1], vc[1], scaling)
+    assert_close(np32(got["out0"]).reshape(H, 128)[idx], o0, what=f"{what} loop-1 output")
+    assert_close(np32(got["out1"]).reshape(H, 128)[idx], o1, what=f"{what} loop-2 output")
+    g_lg = np32(got["logits1"]).reshape(H, -1)[idx, : T + 1]
+    cap = got["indices"].shape[-1]
+    sel = OA.decode_topk(list(g_lg), fraction, kpad=cap)
+    assert np.array_equal(got["indices"].cpu().numpy().reshape(H, cap)[idx], sel.indices), f"{what}: selection"
+    lengths = [T] * len(rows)
+    so = OA.selected_value_aggregate(sel.indices, sel.valid, sel.selected_weights, Vr[1], vc[1], lengths)
+    for loop in (2, 3):
+        want = OA.sparse_delta(q[loop], Kr[loop], Vr[loop], kc[loop], vc[loop], lengths, sel.indices, sel.valid,
+                               so, sel.mass, scaling)
+        assert_close(np32(got[f"delta{loop}"]).reshape(H, 128)[idx], want, what=f"{what} loop-{loop + 1} delta")
+    return chain, tp

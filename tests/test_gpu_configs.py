@@ -3,8 +3,9 @@
 cfg0: B1 H16 T2048, one dense decode step over all four loops, fp32 outputs vs the oracle.
 cfg1: T8192 followed by 256 decode appends (a rollover every 64): the packed streams equal
       the oracle's encoding of the whole 8448-token sequence, and a decode step over the
-      rolled cache matches the oracle.  Heads are reduced to 2 to keep the CPU oracle in
-      seconds; each head is encoded independently, so H does not change the arithmetic.
+      rolled cache matches the oracle (H2); and at H16 a decode step before every append,
+      checked against the oracle after each of the four rollovers (three heads; each head
+      is encoded independently, so a subset of heads is exact).
 cfg2: B32 H16, per-sequence contexts drawn from U[1024, 16384] (seeded): one decode step
       over the full ragged batch on the GPU; every head of the shortest and of the longest
       sequence is checked against the oracle.
@@ -29,6 +30,7 @@ from flashloop_amd.synthetic import SCALING, decode_workload, ragged_lengths
 
 from gpu_util import (
     assert_close,
+    step_vs_oracle_rows,
     assert_layer_matches_chain,
     flat_rows,
     materialized,
@@ -113,6 +115,56 @@ def test_cfg1_appends_and_rollover():
         want = OA.sparse_delta(q[loop], Kr[loop], Vr[loop], kcn[loop], vcn[loop], lengths, sel.indices, sel.valid,
                                so, sel.mass, SCALING)
         assert_close(np32(got).reshape(H, 128), want, what=f"cfg1 loop-{loop + 1} delta")
+
+
+def test_cfg1_decode_every_step_across_rollovers():
+    """BASELINE config 1 as configured: B1 H16 T8192, 256 consecutive decode steps, each a
+    full 4-loop decode step over the cache followed by the append of its token (a tail
+    rollover every 64 appends).  The step after each of the four rollovers (steps 64,
+    128, 192, 256) is checked against the oracle at heads 0, 7 and 15, and at the end
+    the packed streams of those heads equal the oracle's encoding of all 8448 tokens."""
+    print("case: cfg1 H16 T8192, decode + append x256", flush=True)
+    H, T, steps = 16, 8192, 256
+    heads = [0, 7, 15]
+    w = decode_workload(1, H, T, seed=11, extra=steps + 1)
+    keys = [w.keys[r][:, :, :T].contiguous() for r in range(4)]
+    values = [w.values[r][:, :, :T].contiguous() for r in range(4)]
+    layer = _layer(keys, values, token_capacity=T + steps + 64)
+    gen = torch.Generator().manual_seed(111)
+    rolled = []
+    checked = 0
+    for i in range(steps + 1):
+        p = T + i
+        qs = [torch.randn((1, H, 1, 128), generator=gen).to(torch.bfloat16) for _ in range(4)]
+        kc = [w.keys[r][:, :, p:p + 1] for r in range(4)]
+        vc = [w.values[r][:, :, p:p + 1] for r in range(4)]
+        step = decode_attention_step(layer, [x.to(DEV) for x in qs], [k.to(DEV) for k in kc],
+                                     [v.to(DEV) for v in vc], SCALING, 0.10)
+        if i in (64, 128, 192, 256):
+            torch.cuda.synchronize()
+            assert layer.quantized_tokens == codec.packed_prefix_tokens(p), f"step {i}"
+            nk = [np32(w.keys[r][:, heads, :p]) for r in range(4)]
+            nv = [np32(w.values[r][:, heads, :p]) for r in range(4)]
+            q = [np32(x)[0, heads].reshape(len(heads), 128) for x in qs]
+            kcn = [np32(k)[0, heads].reshape(len(heads), 128) for k in kc]
+            vcn = [np32(v)[0, heads].reshape(len(heads), 128) for v in vc]
+            got = dict(out0=step.out0, out1=step.out1, logits1=step.logits1, indices=step.indices,
+                       delta2=step.delta2, delta3=step.delta3)
+            chain, tp = step_vs_oracle_rows(got, heads, H, nk, nv, None, q, kcn, vcn, SCALING, 0.10,
+                                            what=f"cfg1 step {i}")
+            checked += 1
+        else:
+            assert bool(torch.isfinite(step.out1).all()) and bool(torch.isfinite(step.delta3).all()), f"step {i}"
+        if i < steps:
+            before = layer.quantized_tokens
+            layer.append_decode_token([k.to(DEV) for k in kc], [v.to(DEV) for v in vc])
+            if layer.quantized_tokens != before:
+                rolled.append(i)
+    torch.cuda.synchronize()
+    assert rolled == [63, 127, 191, 255] and checked == 4
+    # the packed streams of the checked heads, after the last rollover
+    assert tp == layer.quantized_tokens
+    assert_layer_matches_chain(layer, chain, tp, 1, len(heads), row_ids=heads)
 
 
 def _check_rows(w, layer, step, rows, H, lengths, what):

@@ -203,12 +203,18 @@ def test_graph_recapture_releases_old_graphs():
 
 def test_cfg4_full_model_prefill_and_decode():
     """BASELINE config 4 at its shape: the random-init 24-layer looped decoder (hidden
-    2048, 16 heads x 128, SwiGLU 5632, vocab 49152), an 8192-token prompt, then 70 greedy
-    decode steps (one rollover of the BF16 tail).  Checks the prefill receipts, the
-    loop-2 key budget ceil((T+1)*0.1) actually selected by the top-k kernel at every step,
-    finite logits, graph replay equal to eager launches bit for bit, and each step's
-    logits against the torch-module decode step (fused_decode=False) by cosine."""
-    print("case: cfg4 24L/2048/5632/49152, prompt 8192, 70 steps", flush=True)
+    2048, 16 heads x 128, SwiGLU 5632, vocab 49152), an 8192-token prompt, then 256 greedy
+    decode steps (four rollovers of the BF16 tail, at steps 63, 127, 191 and 255).
+    Checks the prefill receipts, the loop-2 key budget ceil((T+1)*0.1) actually selected
+    by the top-k kernel at every step, finite logits, graph replay equal to eager
+    launches bit for bit, the first 70 steps' logits against the torch-module decode step
+    (fused_decode=False) by cosine, and -- sharing no reader with the engine -- layer 0's
+    attention at the steps after the first three rollovers and at the last step, against
+    the oracle run on layer 0's own K/V history (prefill K/V and masks, then every
+    decoded token), with the packed streams of layer 0 bit-exact after the last rollover."""
+    from gpu_util import assert_layer_matches_chain, np32, step_vs_oracle_rows
+
+    print("case: cfg4 24L/2048/5632/49152, prompt 8192, 256 steps", flush=True)
     cfg = OuroConfig()
     assert (cfg.num_hidden_layers, cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size) == (24, 2048, 5632, 49152)
     model = OuroForCausalLM.random_init(cfg, seed=4, device="cuda")
@@ -218,42 +224,132 @@ def test_cfg4_full_model_prefill_and_decode():
     eager = FlashLoopEngine(model, use_graphs=False)
     modules = FlashLoopEngine(model, use_graphs=False)
     modules.fused_decode = False
-    outs = [e.prefill(ids, decode_capacity=128) for e in (graphed, eager, modules)]
+    heads = [0, 9]  # layer-0 heads held against the oracle
+    # layer 0's prefill K/V and masks, as the eager engine packs them
+    pre = {}
+    from flashloop_amd import cache as cache_mod
+
+    orig_fp = cache_mod.CrossLoopKVLayer.from_prefill.__func__
+
+    def capture_prefill(cls, keys, values, **kw):
+        if not pre:
+            pre["k"] = [np32(k[:, heads]) for k in keys]
+            pre["v"] = [np32(v[:, heads]) for v in values]
+            pre["m"] = (kw["mask_loop3"].cpu().numpy().astype(bool), kw["mask_loop4"].cpu().numpy().astype(bool))
+        return orig_fp(cls, keys, values, **kw)
+
+    outs = [graphed.prefill(ids, decode_capacity=320)]
+    cache_mod.CrossLoopKVLayer.from_prefill = classmethod(capture_prefill)
+    try:
+        outs.append(eager.prefill(ids, decode_capacity=320))
+    finally:
+        cache_mod.CrossLoopKVLayer.from_prefill = classmethod(orig_fp)
+    outs.append(modules.prefill(ids, decode_capacity=320))
     for o in outs:
         assert [(r.loop, r.total_rows, r.active_rows) for r in o.state.prefill_receipts] == \
             [(1, 8192, 8192), (2, 8192, 8192), (3, 8192, 2048), (4, 8192, 820)]
         assert torch.isfinite(o.logits).all()
     assert torch.equal(outs[0].logits, outs[1].logits)
+    assert pre["k"][0].shape == (1, 2, 8192, 128)
     lc = eager.state.cache.layers[0]
     assert lc.quantized_tokens == 8128
     seen = []
-    orig = lc.dense_source_attention_select
+    rec = {}  # this step's layer-0 attention inputs and outputs, per loop
+
+    def keep(loop, kw):
+        rec[loop] = {n: kw[n].detach().clone() for n in ("query", "current_key", "current_value")}
+
+    orig_dense, orig_sel = lc.dense_source_attention, lc.dense_source_attention_select
+    orig_src, orig_delta = lc.cached_mass_sparse_attention_delta_with_source, lc.cached_mass_sparse_attention_delta
     check_sel = lc.select_decode_keys
 
-    def spy(loop, **kw):
-        res = orig(loop, **kw)
-        check_sel(res[1], kw["fraction"], validate=True)  # NaN/inf logits would raise here
-        seen.append(res[2][4])
+    def spy_dense(loop, **kw):
+        res = orig_dense(loop, **kw)
+        keep(loop, kw)
+        rec[loop]["out"] = res[0].clone()
         return res
 
-    lc.dense_source_attention_select = spy
+    def spy_sel(loop, **kw):
+        res = orig_sel(loop, **kw)
+        check_sel(res[1], kw["fraction"], validate=True)  # NaN/inf logits would raise here
+        seen.append(res[2][4])
+        keep(loop, kw)
+        rec[loop].update(out=res[0].clone(), logits=res[1].clone(), indices=res[2][0].clone())
+        return res
+
+    def spy_src(loop, **kw):
+        res = orig_src(loop, **kw)
+        keep(loop, kw)
+        rec[loop]["out"] = res[0].clone()
+        return res
+
+    def spy_delta(loop, **kw):
+        res = orig_delta(loop, **kw)
+        keep(loop, kw)
+        rec[loop]["out"] = res.clone()
+        return res
+
+    lc.dense_source_attention, lc.dense_source_attention_select = spy_dense, spy_sel
+    lc.cached_mass_sparse_attention_delta_with_source, lc.cached_mass_sparse_attention_delta = spy_src, spy_delta
+    hist_k = [[] for _ in range(4)]  # layer-0 K/V of every decoded token, per loop
+    hist_v = [[] for _ in range(4)]
     tok = torch.argmax(outs[0].logits, dim=-1, keepdim=True)
     worst = 1.0
-    for step in range(70):
+    rolled = []
+    checked = []
+    steps = 256
+    for step in range(steps):
         pos = 8192 + step
         a = graphed.decode(tok)
+        before = lc.quantized_tokens
         b = eager.decode(tok)
-        c = modules.decode(tok)
+        if step < 70:
+            c = modules.decode(tok)
+            worst = min(worst, _cos(b.logits, c.logits))
+            assert _cos(b.logits, c.logits) > 0.999, f"step {step}: fused vs torch-module step"
+        elif step == 70:
+            modules.reset()
         assert torch.isfinite(a.logits).all()
         assert torch.equal(a.logits, b.logits), f"step {step}: graph replay differs from eager"
-        worst = min(worst, _cos(b.logits, c.logits))
-        assert _cos(b.logits, c.logits) > 0.999, f"step {step}: fused vs torch-module step"
         want_k = math.ceil((pos + 1) * 0.1)  # T = pos keys before the current token
         assert a.receipt.selected_keys_per_layer == (want_k,) * 24
         assert seen[-1].cpu().tolist() == [want_k] * 16, f"step {step}: observed top-k budget"
+        if step in (64, 128, 192, steps - 1):
+            torch.cuda.synchronize()
+            T = pos
+            nk = [np.concatenate([pre["k"][r]] + [x[None, :, None] for x in hist_k[r]], axis=2) for r in range(4)]
+            nv = [np.concatenate([pre["v"][r]] + [x[None, :, None] for x in hist_v[r]], axis=2) for r in range(4)]
+            assert nk[0].shape[2] == T
+            ones = np.ones((1, step), bool)
+            masks = (np.concatenate([pre["m"][0], ones], 1), np.concatenate([pre["m"][1], ones], 1))
+            sub = lambda t: np32(t).reshape(16, 128)[heads]  # noqa: E731
+            got = dict(out0=rec[0]["out"], out1=rec[1]["out"], logits1=rec[1]["logits"], indices=rec[1]["indices"],
+                       delta2=rec[2]["out"], delta3=rec[3]["out"])
+            step_vs_oracle_rows(got, heads, 16, nk, nv, masks, [sub(rec[r]["query"]) for r in range(4)],
+                                [sub(rec[r]["current_key"]) for r in range(4)],
+                                [sub(rec[r]["current_value"]) for r in range(4)], model.model.layers[0].self_attn.scaling,
+                                0.10, what=f"cfg4 layer 0 step {step}")
+            checked.append(step)
+        for r in range(4):
+            hist_k[r].append(np32(rec[r]["current_key"]).reshape(16, 128)[heads])
+            hist_v[r].append(np32(rec[r]["current_value"]).reshape(16, 128)[heads])
+        if lc.quantized_tokens != before:
+            rolled.append(step)
         tok = torch.argmax(a.logits, dim=-1, keepdim=True)
-    print(f"[parity] cfg4 worst cosine fused vs modules {worst:.6f}", flush=True)
-    assert lc.quantized_tokens == 8192  # one 64-token group rolled out of the tail
+    print(f"[parity] cfg4 worst cosine fused vs modules {worst:.6f} (70 steps)", flush=True)
+    assert rolled == [63, 127, 191, 255] and checked == [64, 128, 192, 255]
+    assert lc.quantized_tokens == 8384  # four 64-token groups rolled out of the tail
+    # layer 0's packed streams (heads 0 and 9) after the fourth rollover, against the oracle
+    # encoding of its whole K/V history
+    from oracle import codec
+
+    nk = [np.concatenate([pre["k"][r]] + [x[None, :, None] for x in hist_k[r]], axis=2) for r in range(4)]
+    nv = [np.concatenate([pre["v"][r]] + [x[None, :, None] for x in hist_v[r]], axis=2) for r in range(4)]
+    ones = np.ones((1, steps), bool)
+    masks = (np.concatenate([pre["m"][0], ones], 1), np.concatenate([pre["m"][1], ones], 1))
+    chain, tp = codec.compress_prefix(nk, nv, masks)  # 8448 tokens: 8384 packed, 64 in the tail
+    assert tp == lc.quantized_tokens
+    assert_layer_matches_chain(lc, chain, tp, 1, len(heads), row_ids=heads)
 
 
 def test_hooks_route_forward_and_generate_with_observed_counters(tmp_path):
