@@ -34,10 +34,25 @@ sys.path.insert(0, ROOT)
 
 METRIC = "int4 KV-residual decode attn µs/step + HBM GB/s (%peak) at 32K ctx, bs=8"
 HBM_PEAK_GBPS = 8000.0
-# HBM bytes per launch of the dense reader kernel (the loop-2 launch, or the loops 1+2
-# pair launch), measured with rocprofv3 FETCH_SIZE (x2.0 calibration against a 1 GiB
-# copy) + WRITE_SIZE on MI355X; summary in profiles/decode_step_cfg3.md.
-MEASURED_TRAFFIC = {"cfg3": (1211.3 + 17.5) * 1e6, "cfg3-pair": (1812.1 + 17.6) * 1e6}
+# HBM bytes per launch of the dense reader kernel, from the rocprofv3 counter runs
+# (FETCH_SIZE x2.0 calibration against a 1 GiB copy, + WRITE_SIZE) summarised in this
+# file, which names its command and the build it was taken on.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "traffic_dense_reader_cfg3.txt")
+
+
+def traffic_from_profile(kernel_key: str):
+    """(bytes per launch, source) of ``kernel_key`` from TRAFFIC_PROFILE, or (None, reason)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 3 and parts[0] == "traffic_bytes" and parts[1] == kernel_key:
+                    build = next((l.split(":", 1)[1].strip() for l in open(TRAFFIC_PROFILE) if l.startswith("build:")),
+                                 "unknown")
+                    return int(parts[2]), f"{os.path.relpath(TRAFFIC_PROFILE, ROOT)} (counter runs on build {build})"
+    except OSError:
+        return None, "no counter profile in this tree"
+    return None, f"no {kernel_key} line in {os.path.relpath(TRAFFIC_PROFILE, ROOT)}"
 CONFIGS = {
     "cfg3": dict(batch=8, heads=16, tokens=32768, seed=3),
     "cfg1": dict(batch=1, heads=16, tokens=8192, seed=1),
@@ -266,9 +281,8 @@ def main():
     elapsed = time.perf_counter() - t0
     ms_step = elapsed / args.steps * 1e3
     # a second timed region of K steps for the roofline: the library records a HIP event
-    # pair on the launch stream around the dense reader kernel of every step.  Each event
-    # is a marker packet that holds the next dispatch back by ~6 us (kernel trace), so it
-    # stays out of the metric's region.
+    # pair on the dense reader kernel's own dispatch in every step (hipExtLaunchKernel),
+    # kept out of the metric's region all the same.
     _lib.check(lib.fl_profile_dense_reader(1 if (not args.paired_dense) else 4, args.steps), "fl_profile_dense_reader")
     t1 = time.perf_counter()
     for i in range(args.steps):
@@ -302,6 +316,8 @@ def main():
     gbps = step_bytes / (ms_step * 1e-3) / 1e9
     reader_bytes = parts["dense_loop2"] + (0 if (not args.paired_dense) else parts["dense_loop1"])
     reader_gbps = reader_bytes / (reader_ms * 1e-3) / 1e9
+    traffic = traffic_from_profile("dense_pair_kernel" if args.paired_dense else "dense_reader_kernel<2,true>") \
+        if args.config == "cfg3" else (None, "counter profile taken at cfg3 only")
     finite = all(bool(torch.isfinite(t).all()) for t in (ref.out0, ref.out1, ref.delta2, ref.delta3))
 
     # per-op breakdown after the timed region: each op of the step (its reader and merge
@@ -403,12 +419,13 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(reader_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": MEASURED_TRAFFIC.get(args.config if (not args.paired_dense) else args.config + "-pair"),
+            "traffic": traffic[0],
+            "traffic_source": traffic[1],
             "algorithmic_bytes": reader_bytes,
             "avg_us": round(reader_ms * 1e3, 2),
-            "timing": (f"HIP event pair on the launch stream around the kernel in each of {args.steps} steps "
-                       f"timed after the metric's region ({round(ms_step_instrumented * 1e3, 2)} us/step with "
-                       "the events)"),
+            "timing": (f"HIP event pair on the kernel's own dispatch (hipExtLaunchKernel, launch stream) in each "
+                       f"of {args.steps} steps timed after the metric's region "
+                       f"({round(ms_step_instrumented * 1e3, 2)} us/step with the events)"),
         },
         "cpu_baseline": cpu,
         "breakdown_bytes": parts,

@@ -18,6 +18,8 @@
 #include "dense_layout.h"
 #include "internal.h"
 
+#include <hip/hip_ext.h>
+
 #include <mutex>
 #include <vector>
 
@@ -780,11 +782,16 @@ int occupancy_of(int loop, bool logits) {
 constexpr int kMaxResident = 2;  // workgroups per CU any reader instantiation can hold
 constexpr int kProfilePair = 4;  // fl_profile_dense_reader code of the pair launch
 
-// ---- measurement hook (fl_profile_dense_reader): HIP events around the reader kernel
+// ---- measurement hook (fl_profile_dense_reader): a HIP event pair on the reader kernel's
+// own dispatch (hipExtLaunchKernel: the events take the kernel's start and end times, with
+// no marker packet before or after it on the stream)
 struct ReaderProfile {
   int loop = -1, want = 0, used = 0;
   bool armed = false;  // the current call records (set by profile_before)
   std::vector<hipEvent_t> start, stop;
+};
+struct EventPair {
+  hipEvent_t start = nullptr, stop = nullptr;
 };
 std::mutex g_prof_mu;
 ReaderProfile g_prof;
@@ -795,20 +802,31 @@ void profile_free() {
   g_prof = ReaderProfile{};
 }
 
-void profile_before(hipStream_t st, int loop) {
+// The event pair this launch records into (none: not profiling, or under capture).
+EventPair profile_before(hipStream_t st, int loop) {
   std::lock_guard<std::mutex> g(g_prof_mu);
   g_prof.armed = false;
-  if (g_prof.used >= g_prof.want || (g_prof.loop >= 0 && g_prof.loop != loop)) return;
+  if (g_prof.used >= g_prof.want || (g_prof.loop >= 0 && g_prof.loop != loop)) return {};
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
-  if (hipEventRecord(g_prof.start[g_prof.used], st) == hipSuccess) g_prof.armed = true;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return {};
+  g_prof.armed = true;
+  return EventPair{g_prof.start[g_prof.used], g_prof.stop[g_prof.used]};
 }
 
-void profile_after(hipStream_t st) {
+void profile_after(bool launched) {
   std::lock_guard<std::mutex> g(g_prof_mu);
   if (!g_prof.armed) return;
   g_prof.armed = false;
-  if (hipEventRecord(g_prof.stop[g_prof.used], st) == hipSuccess) ++g_prof.used;
+  if (launched) ++g_prof.used;
+}
+
+// Launch of one reader kernel, on its own events when profiling.
+template <typename K, typename... Args>
+void launch_reader(K kernel, dim3 grid, dim3 block, hipStream_t st, const EventPair& ev, Args... args) {
+  if (ev.start)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, st, ev.start, ev.stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, args...);
 }
 
 // Persistent grid: every resident 4-wave workgroup slot of the GPU, fewer when the
@@ -931,19 +949,19 @@ int32_t dense_launch(const fl_cache_view& v, int32_t loop, const uint16_t* q, co
   // a row has at most waves + 1 prefix partials (see partial_slot) plus its tail partial
   FL_REQUIRE(a.waves + 2 <= kMergeMaxParts, "fl_decode_attn_dense: too many persistent waves for one merge");
   const dim3 grid(blocks), block(kThreads);
-  profile_before(st, loop);
+  const EventPair ev = profile_before(st, loop);
   const bool lg = logits != nullptr;
   switch (loop * 2 + (lg ? 1 : 0)) {
-    case 0: hipLaunchKernelGGL((dense_reader_kernel<1, false>), grid, block, 0, st, a); break;
-    case 1: hipLaunchKernelGGL((dense_reader_kernel<1, true>), grid, block, 0, st, a); break;
-    case 2: hipLaunchKernelGGL((dense_reader_kernel<2, false>), grid, block, 0, st, a); break;
-    case 3: hipLaunchKernelGGL((dense_reader_kernel<2, true>), grid, block, 0, st, a); break;
-    case 4: hipLaunchKernelGGL((dense_reader_kernel<3, false>), grid, block, 0, st, a); break;
-    case 5: hipLaunchKernelGGL((dense_reader_kernel<3, true>), grid, block, 0, st, a); break;
-    case 6: hipLaunchKernelGGL((dense_reader_kernel<4, false>), grid, block, 0, st, a); break;
-    default: hipLaunchKernelGGL((dense_reader_kernel<4, true>), grid, block, 0, st, a); break;
+    case 0: launch_reader(dense_reader_kernel<1, false>, grid, block, st, ev, a); break;
+    case 1: launch_reader(dense_reader_kernel<1, true>, grid, block, st, ev, a); break;
+    case 2: launch_reader(dense_reader_kernel<2, false>, grid, block, st, ev, a); break;
+    case 3: launch_reader(dense_reader_kernel<2, true>, grid, block, st, ev, a); break;
+    case 4: launch_reader(dense_reader_kernel<3, false>, grid, block, st, ev, a); break;
+    case 5: launch_reader(dense_reader_kernel<3, true>, grid, block, st, ev, a); break;
+    case 6: launch_reader(dense_reader_kernel<4, false>, grid, block, st, ev, a); break;
+    default: launch_reader(dense_reader_kernel<4, true>, grid, block, st, ev, a); break;
   }
-  profile_after(st);
+  profile_after(hipPeekAtLastError() == hipSuccess);
   FL_LAUNCH_CHECK("fl_decode_attn_dense(reader)");
   if (waves) *waves = a.waves;
   if (!merge) return FL_OK;
@@ -1092,9 +1110,9 @@ extern "C" int32_t fl_decode_attn_dense_pair(const fl_cache_view* view, const ui
   }
   FL_REQUIRE(a[0].waves + 2 <= kMergeMaxParts, "fl_decode_attn_dense_pair: too many persistent waves for one merge");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  profile_before(st, kProfilePair);
-  hipLaunchKernelGGL(dense_pair_kernel, dim3(blocks), dim3(kThreads), 0, st, a[0], a[1]);
-  profile_after(st);
+  const EventPair ev = profile_before(st, kProfilePair);
+  launch_reader(dense_pair_kernel, dim3(blocks), dim3(kThreads), st, ev, a[0], a[1]);
+  profile_after(hipPeekAtLastError() == hipSuccess);
   FL_LAUNCH_CHECK("fl_decode_attn_dense_pair(reader)");
   hipLaunchKernelGGL(dense_merge_kernel, dim3(2 * v.batch * v.heads), dim3(kMergeThreads), 0, st,
                      static_cast<const float*>(a[0].ws), static_cast<const float*>(a[1].ws), a[0].waves, v, out0, out1, 2);

@@ -190,8 +190,9 @@ int32_t fl_decode_attn_dense_pair(const fl_cache_view* view,
 
 /*
  * Measurement hook (no counterpart in the reference; for benchmarks): record a pair of
- * HIP events on the launch stream immediately around the reader kernel (not the merge)
- * of the next `launches` calls of fl_decode_attn_dense with this `loop` index (-1: any).
+ * HIP events on the reader kernel's own dispatch (not the merge; hipExtLaunchKernel, so
+ * the events carry the kernel's start and end and no marker packet runs beside it) for
+ * the next `launches` calls of fl_decode_attn_dense with this `loop` index (-1: any).
  * `launches` = 0 stops recording and frees the events.  Calls made while the stream is
  * being captured into a graph are not recorded.  fl_profile_dense_reader_read waits
  * for the recorded events and returns the summed elapsed time and the number of
