@@ -526,6 +526,66 @@ def test_decode_append_and_rollover_bit_exact():
     assert_close(np32(out).reshape(2, 128), want, what="post-rollover output")
 
 
+def test_rollover_refused_at_row_capacity_changes_nothing():
+    """A rollover that would overflow a loop-3/4 row capacity (the exact read-back check)
+    raises before any device change: rank maps, row counts, lengths and codes are as
+    before, and after the capacity is restored a retried rollover leaves the layer equal
+    to one that never hit the limit (no row is counted twice)."""
+    import dataclasses
+
+    print("case: rollover at row capacity", flush=True)
+    B, H, t0 = 2, 1, 200
+    w = decode_workload(B, H, t0, seed=31, extra=80)
+    m3, m4 = _masks(B, t0, 31)
+
+    def build():
+        ks = [w.keys[r][:, :, :t0].contiguous().to(DEV) for r in range(4)]
+        vs = [w.values[r][:, :, :t0].contiguous().to(DEV) for r in range(4)]
+        return CrossLoopKVLayer.from_prefill(ks, vs, mask_loop3=torch.from_numpy(m3).to(DEV),
+                                             mask_loop4=torch.from_numpy(m4).to(DEV), token_capacity=t0 + 128)
+
+    def append(layer, p, commit=True):
+        args = ([w.keys[r][:, :, p:p + 1].to(DEV) for r in range(4)],
+                [w.values[r][:, :, p:p + 1].to(DEV) for r in range(4)])
+        if commit:
+            layer.append_decode_token(*args)
+        else:
+            layer.append_rows(*args)
+
+    limited, free = build(), build()
+    assert limited.tail_host == [72, 72]
+    for i in range(55):  # the 56th append fills the tails and rolls a group out
+        append(limited, t0 + i)
+        append(free, t0 + i)
+    late = limited.late_rows_host
+    g0 = limited.geometry
+    # loop 4 (stream 3) can take only 5 more rows in any sequence; loop 3 has room
+    limited.geometry = dataclasses.replace(g0, row_capacity=(*g0.row_capacity[:3], max(late[1]) + 5))
+    snap = dict(rank=[r.clone() for r in limited.rank], late=limited.late_rows.clone(),
+                packed=limited.packed_tokens.clone(), codes=[c.clone() for c in limited.codes])
+    append(limited, t0 + 55, commit=False)
+    with pytest.raises(RuntimeError, match="row capacity exhausted"):
+        limited.commit_append()
+    torch.cuda.synchronize()
+    for a_, b_ in zip(limited.rank, snap["rank"]):
+        assert torch.equal(a_, b_)
+    assert torch.equal(limited.late_rows, snap["late"]) and torch.equal(limited.packed_tokens, snap["packed"])
+    for a_, b_ in zip(limited.codes, snap["codes"]):
+        assert torch.equal(a_, b_)
+    assert limited.packed_host == [128, 128]
+    # capacity restored: the retried rollover equals the rollover of the unlimited layer
+    limited.geometry = g0
+    limited._roll_groups()
+    append(free, t0 + 55)
+    torch.cuda.synchronize()
+    assert limited.packed_host == free.packed_host == [192, 192] and limited.tail_host == free.tail_host
+    assert limited.late_rows_host == free.late_rows_host
+    for s in range(4):
+        assert torch.equal(limited.codes[s], free.codes[s])
+    for a_, b_ in zip(limited.rank, free.rank):
+        assert torch.equal(a_, b_)
+
+
 def test_rows_gather_scatter_round_trip():
     print("case: rows", flush=True)
     g = torch.Generator().manual_seed(0)
