@@ -583,7 +583,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
   float invZ = 0.0f;
   uint32_t kmin = kScoreKeyFloor, shift = 31u, binmax = 0u;  // a score-ordered row: one bin
   if (weighted) {
-    float z = 0.0f;
+    float z = 0.0f;  // (padding's -inf adds +0)
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const float e = softmax_exp(__uint_as_float(kr[j]) - M);
@@ -604,13 +604,14 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
     for (int j = 0; j < PER; ++j) kr[j] = index_of(j) < n ? score_key(__uint_as_float(kr[j])) : 0u;
   }
 
-  // ---- 3. histogram: bin(key) is non-decreasing in the key (and 0 for padding)
+  // ---- 3. histogram: bin(key) is non-decreasing in the key.  Padding is not counted: a
+  // row's padding all on one bin would serialise its LDS atomics.
   uint32_t* lin = &sh.hist[0][0];  // one kBins-bin histogram (the sub-histograms are for the radix)
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int b = static_cast<int>(min(static_cast<uint32_t>(max(static_cast<int>(kr[j] - kmin), 0)) >> shift, binmax));
     sh.bin[j][tid] = static_cast<uint16_t>(b);
-    atomicAdd(&lin[b], 1u);
+    if (kr[j] != 0u) atomicAdd(&lin[b], 1u);
   }
   __syncthreads();  // the histogram is complete
   // Only a row holding a non-finite score (the same decision in every thread) counts
@@ -622,7 +623,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
   }
   {
     const int bin = kBins - 1 - tid;  // descending scan: thread t owns bin kBins-1-t
-    const uint32_t h = lin[bin] - (bin == 0 ? static_cast<uint32_t>(PER * kTopkThreads - n) : 0u);
+    const uint32_t h = lin[bin];
     uint32_t incl = h;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -649,6 +650,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
     uint32_t c = 0;
+    if (q * kQuadChunk >= n) continue;  // (row-uniform) a chunk past the row's keys
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int j = 4 * q + e;
@@ -811,6 +813,7 @@ __device__ __forceinline__ void topk_resident_row(ResShared& sh, KeyCount key_co
   const uint32_t base_lane = lane < Q ? sh.cnt[lane][w] : 0u;  // lane q: offset of chunk q
 #pragma unroll
   for (int q = 0; q < Q; ++q) {
+    if (q * kQuadChunk >= n) continue;  // (row-uniform) no key of this chunk is selected
     bool sel[4];
     uint32_t before = 0;
 #pragma unroll
