@@ -182,10 +182,9 @@ class DecodeRunner:
                 lc.tail_tokens -= 1
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        # Unreachable objects that own a graph (another engine's, say) must be destroyed
-        # before the capture, not by a collection the capture's allocations trigger: a
-        # graph destroyed while a stream captures aborts the process.
-        gc.collect()
+        # A graph destroyed while a stream captures aborts the process, so no garbage
+        # collection may run during the capture (one triggered by the capture's own
+        # allocations could free an unreachable object that owns a graph).
         was_enabled = gc.isenabled()
         gc.disable()
         try:
