@@ -113,6 +113,7 @@ struct TopkShared {
   uint32_t sel_remaining;
   uint32_t bin_above;
   uint32_t nonfin;
+  uint32_t has_nan;
 };
 
 __device__ float block_max(float v, TopkShared& sh) {
@@ -271,7 +272,10 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
     return;
   }
   // softmax statistics of the row (flashloop/engine.py:440-442) and its non-finite scores
-  if (threadIdx.x == 0) sh.nonfin = 0;
+  if (threadIdx.x == 0) {
+    sh.nonfin = 0;
+    sh.has_nan = 0;
+  }
   float mx = -INFINITY;
   uint32_t nf = 0, amax = 0;
   for (int i = threadIdx.x; i < n; i += kTopkThreads) {
@@ -282,12 +286,9 @@ __global__ __launch_bounds__(kTopkThreads) void decode_topk_kernel(const float* 
   }
   const float M = block_max(mx, sh);  // (its barriers order the counter's reset)
   if (nf) atomicAdd(&sh.nonfin, nf);
-  // NaN anywhere is flagged through the count of keys above inf's bits
-  if (amax > 0x7F800000u) atomicOr(&sh.nonfin, 0x40000000u);
+  if (amax > 0x7F800000u) sh.has_nan = 1u;  // |x|'s bits above inf's: a NaN
   __syncthreads();
-  const bool weighted = (sh.nonfin & 0x40000000u) == 0u && M > -INFINITY && M < INFINITY;
-  __syncthreads();
-  if (threadIdx.x == 0) sh.nonfin &= 0x3FFFFFFFu;
+  const bool weighted = sh.has_nan == 0u && M > -INFINITY && M < INFINITY;
   // the same weight image and summation order as the register-resident kernel: thread t
   // sums indices q*4096 + 4t + e in (q, e) order, then the fixed-order block sum
   float invZ = 0.0f;
