@@ -55,7 +55,10 @@ def traffic_from_profile(kernel_key: str):
     return None, f"no {kernel_key} line in {os.path.relpath(TRAFFIC_PROFILE, ROOT)}"
 CONFIGS = {
     "cfg3": dict(batch=8, heads=16, tokens=32768, seed=3),
+    "cfg0": dict(batch=1, heads=16, tokens=2048, seed=0),
     "cfg1": dict(batch=1, heads=16, tokens=8192, seed=1),
+    # ragged batch: per-sequence contexts drawn from U[1024, 16384] (seeded)
+    "cfg2": dict(batch=32, heads=16, tokens=16384, seed=2, ragged=(1024, 16384)),
     # end-to-end random-init looped decoder, run through FlashLoopEngine
     "cfg4": dict(prompt=8192, new_tokens=256, seed=4),
 }
@@ -79,6 +82,9 @@ def parse():
                          "once, which the looped model's loop-by-loop order never provides)")
     ap.add_argument("--no-chain", action="store_true",
                     help="cfg4: residual/norm chains as launches of their own, not inside the next GEMV")
+    ap.add_argument("--graph", action="store_true",
+                    help="cfg0-cfg3: the metric's timed region replays the step captured once in a HIP "
+                         "graph (host launch cost out of the step; the small configs are launch-bound)")
     ap.add_argument("--fraction", type=float, default=0.10)
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (a known-size kernel that "
@@ -112,13 +118,16 @@ def cpu_baseline(sample, fraction: float, seconds: float):
 def cpu_sample(ks, vs, queries, kcur, vcur, rows: int, B: int, H: int, T: int):
     """The first ``rows`` (b,h) rows of the workload as the reference's torch path holds
     them: per loop the materialised bf16 cache (the codec's reconstruction of the packed
-    prefix -- built on the GPU, bit-identical to the oracle's -- then the BF16 tail)."""
+    prefix -- built on the GPU, bit-identical to the oracle's -- then the BF16 tail).
+    ``T``: the sampled rows' context length (a ragged batch samples rows of its first
+    sequence only)."""
     import torch
 
     from flashloop_amd import CrossLoopKVLayer
 
-    sub_k = [k.reshape(1, B * H, T, 128)[:, :rows].contiguous() for k in ks]
-    sub_v = [v.reshape(1, B * H, T, 128)[:, :rows].contiguous() for v in vs]
+    Tall = ks[0].shape[2]
+    sub_k = [k.reshape(1, B * H, Tall, 128)[:, :rows, :T].contiguous() for k in ks]
+    sub_v = [v.reshape(1, B * H, Tall, 128)[:, :rows, :T].contiguous() for v in vs]
     small = CrossLoopKVLayer.from_prefill(sub_k, sub_v, recon=True)
     tp = small.quantized_tokens
     keys, values = [], []
@@ -209,10 +218,16 @@ def main():
     B, H, T = cfg["batch"], cfg["heads"], cfg["tokens"]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    lengths = None
+    if "ragged" in cfg:
+        from flashloop_amd.synthetic import ragged_lengths
+
+        lengths = ragged_lengths(B, *cfg["ragged"], seed=cfg["seed"])
+        T = max(lengths)
     print(f"[bench] building {args.config} workload B={B} H={H} T={T} on {torch.cuda.get_device_name(0)}",
           file=sys.stderr, flush=True)
 
-    w = decode_workload(B, H, T, seed=cfg["seed"], device=dev)
+    w = decode_workload(B, H, T, seed=cfg["seed"], device=dev, lengths=lengths)
     cur = [w.current(r) for r in range(4)]
     queries = [q.contiguous() for q in w.queries]
     ks = [w.keys[r][:, :, :T].contiguous() for r in range(4)]
@@ -220,15 +235,17 @@ def main():
     del w
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    layer = CrossLoopKVLayer.from_prefill(ks, vs)
+    layer = CrossLoopKVLayer.from_prefill(ks, vs, lengths=lengths)
     torch.cuda.synchronize()
     pack_s = time.perf_counter() - t0
-    pack_bytes = 8 * B * H * T * 128 * 2  # bf16 inputs of 4 loops K and V (read once)
+    pack_bytes = 8 * H * (B * T if lengths is None else sum(lengths)) * 128 * 2  # bf16 K and V of 4 loops, read once
     kcur = [c[0] for c in cur]
     vcur = [c[1] for c in cur]
     sample = None
     if args.cpu_rows > 0:
-        sample = cpu_sample(ks, vs, queries, kcur, vcur, min(args.cpu_rows, B * H), B, H, T)
+        # (a ragged batch: rows of its first sequence, at that sequence's length)
+        n_rows = min(args.cpu_rows, B * H) if lengths is None else min(args.cpu_rows, H)
+        sample = cpu_sample(ks, vs, queries, kcur, vcur, n_rows, B, H, T if lengths is None else lengths[0])
     del ks, vs
     torch.cuda.empty_cache()
     if args.calib_copy_mib > 0:
@@ -263,10 +280,10 @@ def main():
             idx, valid, mass, wts, counts = layer.select_decode_keys(logits, args.fraction)
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
-            source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)
+            source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING, counts=counts)
         d3 = layer.cached_mass_sparse_attention_delta(3, query=queries[3], current_key=kcur[3], current_value=vcur[3],
                                                       indices=idx, valid=valid, source_selected_output=so,
-                                                      global_mass=mass, scaling=SCALING)
+                                                      global_mass=mass, scaling=SCALING, counts=counts)
         return out0, out1, d2, d3
 
     for _ in range(args.warmup):
@@ -274,9 +291,34 @@ def main():
     ref = step()
     torch.cuda.synchronize()
     # the timed region of the metric: K steps with nothing else on the stream
+    graph = None
+    if args.graph:
+        import gc
+
+        side = torch.cuda.Stream()  # default priority
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            timed_step(-1)  # sizes every workspace outside the capture
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        gc.disable()  # no collection may destroy a graph while the stream captures
+        try:
+            with torch.cuda.graph(graph):
+                g_out = timed_step(-1)
+        finally:
+            gc.enable()
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out0", "out1", "delta2", "delta3"), g_out, (ref.out0, ref.out1, ref.delta2, ref.delta3)):
+            if not torch.equal(a, b):
+                raise RuntimeError(f"graph replay differs from the eager step in {name}")
     t0 = time.perf_counter()
     for i in range(args.steps):
-        timed_step(i)
+        if graph is None:
+            timed_step(i)
+        else:
+            graph.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_step = elapsed / args.steps * 1e3
@@ -325,7 +367,7 @@ def main():
     # events on the launch stream, so the event overhead is paid once per op, not per run
     breakdown = None
     if args.breakdown_steps > 0:
-        idx, valid, mass, wts, _ = layer.select_decode_keys(ref.logits1, args.fraction)
+        idx, valid, mass, wts, counts = layer.select_decode_keys(ref.logits1, args.fraction)
         so = ref.selected_output
         ops = []
         if not args.paired_dense:
@@ -341,10 +383,10 @@ def main():
             ops.append(("topk", lambda: layer.select_decode_keys(ref.logits1, args.fraction)))
         ops.append(("sparse_loop3_with_source", lambda: layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=kcur[2], current_value=vcur[2], indices=idx, valid=valid,
-            source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING)))
+            source_weights=wts, source_current_value=vcur[1], global_mass=mass, scaling=SCALING, counts=counts)))
         ops.append(("sparse_loop4", lambda: layer.cached_mass_sparse_attention_delta(
             3, query=queries[3], current_key=kcur[3], current_value=vcur[3], indices=idx, valid=valid,
-            source_selected_output=so, global_mass=mass, scaling=SCALING)))
+            source_selected_output=so, global_mass=mass, scaling=SCALING, counts=counts)))
         breakdown = {}
         for name, fn in ops:
             fn()
@@ -374,7 +416,10 @@ def main():
         rows = sample[0][0].shape[0]
         print(f"[bench] CPU baseline on {rows} rows", file=sys.stderr, flush=True)
         s_step, dt, reps, threads = cpu_baseline(sample, args.fraction, args.cpu_seconds)
-        us_cpu = s_step * (B * H) / rows * 1e6
+        # scaled by keys: the step's total over the sample's (rows of equal length)
+        all_keys = H * (sum(lengths) if lengths is not None else B * T)
+        sample_keys = rows * (lengths[0] if lengths is not None else T)
+        us_cpu = s_step * all_keys / sample_keys * 1e6
         cpu = {
             "value": round(step_bytes / (us_cpu * 1e-6) / 1e9, 4),
             "unit": "GB/s",
@@ -384,7 +429,8 @@ def main():
             "sample": f"{rows} of {B * H} (b,h) rows of the same workload at full context: flashloop_torch's "
                       f"decode step (oracle/torch_cpu.py: bf16 attention over the materialised caches of all "
                       f"4 loops, top-k mask, mass-scaled sparse outputs) on torch-CPU with {threads} threads, "
-                      f"repeated {reps} times ({dt:.1f} s), scaled by {B * H}/{rows}",
+                      f"repeated {reps} times ({dt:.1f} s), scaled by the step's keys over the sample's "
+                      f"({all_keys}/{sample_keys})",
         }
 
     line = {
@@ -403,13 +449,16 @@ def main():
         "dtype": "int4 codes x fp16 scale/min, f32 accumulate",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.config}: decode attention of one layer, 4 loops, B={B} H={H} D=128 T={T}, "
-                        f"int4 residual streams g64 (fp32 scale/min stored, fp16 copies streamed), BF16 tail {tail[0]}, "
+            "workload": f"{args.config}: decode attention of one layer, 4 loops, B={B} H={H} D=128 "
+                        + (f"T={T}, " if lengths is None else
+                           f"ragged T~U[{cfg['ragged'][0]},{cfg['ragged'][1]}] (seed {cfg['seed']}, max {T}), ")
+                        + f"int4 residual streams g64 (fp32 scale/min stored, fp16 copies streamed), BF16 tail {tail[0]}, "
                         f"late loops on top {args.fraction:.0%} keys",
             "batch": B,
             "heads": H,
-            "context": T,
+            "context": T if lengths is None else lengths,
             "fraction": args.fraction,
+            "launch": "HIP graph replay" if args.graph else "eager (one host launch per kernel)",
         },
         "roofline": {
             "bound": "hbm",

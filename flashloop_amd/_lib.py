@@ -75,14 +75,14 @@ SIGNATURES = {
     "fl_decode_attn_dense_select": (_I32, [_VIEW, _I32, _P, _P, _P, _F32, _P, _P, _I64, _F64, _I32, _P, _P, _P, _P,
                                            _P, _P, _P, _SZ, _P]),
     "fl_decode_selected_workspace": (_SZ, [_VIEW, _I32]),
-    "fl_decode_selected_pv": (_I32, [_VIEW, _I32, _P, _P, _P, _I32, _P, _P, _P, _SZ, _P]),
+    "fl_decode_selected_pv": (_I32, [_VIEW, _I32, _P, _P, _P, _I32, _P, _P, _P, _P, _SZ, _P]),
     "fl_decode_attn_sparse_delta": (
         _I32,
-        [_VIEW, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _F32, _P, _P, _SZ, _P],
+        [_VIEW, _I32, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _F32, _P, _P, _SZ, _P],
     ),
     "fl_decode_attn_sparse_delta_fused": (
         _I32,
-        [_VIEW, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _F32, _P, _P, _P, _SZ, _P],
+        [_VIEW, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P, _P, _F32, _P, _P, _P, _SZ, _P],
     ),
     "fl_gather_rows": (_I32, [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),
     "fl_scatter_rows": (_I32, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P]),

@@ -332,35 +332,53 @@ class CrossLoopKVLayer:
         shape = (self.batch, self.heads, cap)
         return idx.view(shape), valid.view(shape), mass.view(self.batch, self.heads, 1, 1), w.view(shape), counts
 
-    def pv(self, loop: int, weights, indices, valid, current_value):
+    def _reader_counts(self, counts):
+        """The selection counts handed to the sparse readers: only for a ragged batch.  With
+        equal lengths every row's count is within 16 slots of the capacity, the padded
+        partition is already balanced, and the live-tile prefix would only add its latency
+        (a few microseconds per launch).  Lengths grow together during decode, so the choice
+        holds for a captured step's replays; either choice gives the same results."""
+        if counts is None:
+            return None
+        totals = [p + t for p, t in zip(self.packed_host, self.tail_host)]
+        return counts if min(totals) != max(totals) else None
+
+    def pv(self, loop: int, weights, indices, valid, current_value, counts=None):
         """``_selected_value_aggregate`` (flashloop/engine.py:346-371): sum of selected V rows
-        of loop ``loop`` weighted by ``weights``; the current token reads ``current_value``."""
+        of loop ``loop`` weighted by ``weights``; the current token reads ``current_value``.
+        ``counts`` (optional, the selection's i32 ``[B*H]`` counts): every valid slot of a row
+        lies below its count, so the reader skips the padding past it."""
         out = kernels.fused_cross_loop_pv(self.view(), int(loop), indices, valid, weights, current_value,
-                                          device=self.device, workspace=self.workspace)
+                                          device=self.device, workspace=self.workspace,
+                                          counts=self._reader_counts(counts))
         return out.view(self.batch, self.heads, 1, HEAD_DIM)
 
     def cached_mass_sparse_attention_delta(self, loop: int, *, query, current_key, current_value, indices, valid,
-                                           source_selected_output, global_mass, scaling: float):
-        """``CrossLoopKVLayer.cached_mass_sparse_attention_delta`` (flashloop/cache.py:1517-1617)."""
+                                           source_selected_output, global_mass, scaling: float, counts=None):
+        """``CrossLoopKVLayer.cached_mass_sparse_attention_delta`` (flashloop/cache.py:1517-1617);
+        ``counts`` as in ``pv``."""
         if int(loop) not in (2, 3):
             raise ValueError("cached-mass sparse attention is only valid for Loop 3/4")
         out = kernels.fused_sparse_attention_delta(
             self.view(), int(loop), query, current_key, current_value, indices, valid, source_selected_output,
             global_mass, scaling, device=self.device, workspace=self.workspace,
+            counts=self._reader_counts(counts),
         )
         return out.view(self.batch, self.heads, 1, HEAD_DIM)
 
     def cached_mass_sparse_attention_delta_with_source(self, loop: int, *, query, current_key, current_value,
                                                        indices, valid, source_weights, source_current_value,
-                                                       global_mass, scaling: float):
+                                                       global_mass, scaling: float, counts=None):
         """Loop-3 form of ``cached_mass_sparse_attention_delta`` that also returns the loop-2
         selected aggregate (``_selected_value_aggregate``, flashloop/engine.py:346-371) from
-        the same pass over the selected rows.  Returns ``(delta, source_output)``."""
+        the same pass over the selected rows.  Returns ``(delta, source_output)``;
+        ``counts`` as in ``pv``."""
         if int(loop) not in (2, 3):
             raise ValueError("cached-mass sparse attention is only valid for Loop 3/4")
         out, src = kernels.fused_sparse_attention_delta_with_source(
             self.view(), int(loop), query, current_key, current_value, indices, valid, source_weights,
             source_current_value, global_mass, scaling, device=self.device, workspace=self.workspace,
+            counts=self._reader_counts(counts),
         )
         shape = (self.batch, self.heads, 1, HEAD_DIM)
         return out.view(shape), src.view(shape)
@@ -603,8 +621,8 @@ class CrossLoopKVCache:
     def cached_mass_sparse_attention_delta(self, layer_index: int, loop: int, **kwargs):
         return self._require_layer(layer_index).cached_mass_sparse_attention_delta(loop, **kwargs)
 
-    def pv(self, layer_index: int, loop: int, weights, indices, valid, current_value):
-        return self._require_layer(layer_index).pv(loop, weights, indices, valid, current_value)
+    def pv(self, layer_index: int, loop: int, weights, indices, valid, current_value, counts=None):
+        return self._require_layer(layer_index).pv(loop, weights, indices, valid, current_value, counts=counts)
 
     @property
     def storage_bytes(self) -> int:
@@ -686,13 +704,14 @@ def decode_attention_step(layer: CrossLoopKVLayer, queries, keys, values, scalin
     if fused_source:
         d2, so = layer.cached_mass_sparse_attention_delta_with_source(
             2, query=queries[2], current_key=keys[2], current_value=values[2], indices=idx, valid=valid,
-            source_weights=w, source_current_value=values[1], global_mass=mass, scaling=scaling)
+            source_weights=w, source_current_value=values[1], global_mass=mass, scaling=scaling, counts=counts)
     else:
-        so = layer.pv(1, w, idx, valid, values[1])
+        so = layer.pv(1, w, idx, valid, values[1], counts=counts)
         d2 = layer.cached_mass_sparse_attention_delta(2, query=queries[2], current_key=keys[2],
                                                       current_value=values[2], indices=idx, valid=valid,
-                                                      source_selected_output=so, global_mass=mass, scaling=scaling)
+                                                      source_selected_output=so, global_mass=mass, scaling=scaling,
+                                                      counts=counts)
     d3 = layer.cached_mass_sparse_attention_delta(3, query=queries[3], current_key=keys[3], current_value=values[3],
                                                   indices=idx, valid=valid, source_selected_output=so,
-                                                  global_mass=mass, scaling=scaling)
+                                                  global_mass=mass, scaling=scaling, counts=counts)
     return AttentionStep(out0, out1, logits, idx, valid, mass, w, counts, so, d2, d3)

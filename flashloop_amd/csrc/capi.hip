@@ -12,4 +12,4 @@ void clear_error() { g_last_error.clear(); }
 }  // namespace fl
 
 extern "C" const char* fl_last_error(void) { return fl::g_last_error.c_str(); }
-extern "C" int32_t fl_abi_version(void) { return 3; }
+extern "C" int32_t fl_abi_version(void) { return 4; }

@@ -36,6 +36,7 @@ struct GatherArgs {
   const uint16_t* tail_k;  // tail_key[loop] / tail_value[loop] / tail_value[1], resolved on the host
   const uint16_t* tail_v;
   const uint16_t* tail_v1;
+  const int32_t* counts;  // selected slots per row (nullable: every row holds `cap`)
   int cap;
   float scaling;
   float* ws;              // partial slots [waves + B*H] (+ a second set for the fused source aggregate)
@@ -49,6 +50,62 @@ struct GatherArgs {
 
 constexpr int kGatherSegs = 3;   // row segments a wave stages (its first one until the end)
 constexpr int kLenCacheG = 512;  // batches whose lengths a reader caches in LDS
+constexpr int kLiveRows = 2048;  // rows whose live-tile prefix a reader keeps in LDS
+
+// ---------------------------------------------------------------------------------
+// Live tiles.  With per-row selected counts, row r holds max(1, ceil(count_r / T)) live
+// tiles (T slots per tile; count clamped to [0, cap]) and the readers partition only
+// those, so a ragged batch's padding slots cost no wave time; without counts (or beyond
+// kLiveRows rows) every row holds cap / T tiles.  A row keeps at least one tile, so a row
+// with nothing selected still gets its (empty) partial.  The reader and the merge derive
+// the same integers from the same counts.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ int live_tiles(const int32_t* counts, int r, int cap, int tok) {
+  const int c = min(max(counts[r], 0), cap);
+  return max((c + tok - 1) / tok, 1);
+}
+
+__device__ __forceinline__ int wave_sum_int(int x) {
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) x += __shfl_xor(x, d, kWave);
+  return x;
+}
+
+// pre[r] = live tiles of rows 0..r-1, r = 0..rows (kThreads threads; rows <= kLiveRows),
+// in two halves so that a caller can issue other loads between them: live_load reads this
+// thread's rows, live_prefix scans them (and ends with a barrier).
+constexpr int kLivePer = (kLiveRows + kThreads - 1) / kThreads;
+__device__ __forceinline__ void live_load(int* mine, const int32_t* counts, int rows, int cap, int tok) {
+  const int r0 = threadIdx.x * kLivePer;
+#pragma unroll
+  for (int k = 0; k < kLivePer; ++k) mine[k] = r0 + k < rows ? live_tiles(counts, r0 + k, cap, tok) : 0;
+}
+__device__ __forceinline__ void live_prefix(int* pre, int* wave_tot, const int* mine, int rows) {
+  constexpr int kPer = kLivePer;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r0 = tid * kPer;
+  int s = 0;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) s += mine[k];
+  // inclusive scan over the wave, then the earlier waves' totals
+  int x = s;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(x, d, kWave);
+    if (lane >= d) x += y;
+  }
+  if (lane == kWave - 1) wave_tot[tid >> 6] = x;
+  __syncthreads();
+  int base = x - s;
+  for (int w = 0; w < (tid >> 6); ++w) base += wave_tot[w];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    if (r0 + k < rows) pre[r0 + k] = base;
+    base += mine[k];
+  }
+  if (tid == kThreads - 1) pre[rows] = base;  // the last thread's rows end the sequence
+  __syncthreads();
+}
 
 // Partial slot of row bh from workgroup g: a workgroup's tile range is contiguous, so the
 // slots of one row are contiguous and disjoint from every other row's.
@@ -240,11 +297,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int w = blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(wave);
   TileLds<NS, LPT>& L = lds[wave];
   const int rows = v.batch * v.heads;
-  const int tpr = a.cap / Y::kTok;  // tiles per row
-  const int64_t total = static_cast<int64_t>(rows) * tpr;
-  const int64_t chunk = uniform64((total + a.waves - 1) / a.waves);
-  const int64_t t0 = static_cast<int64_t>(w) * chunk;
-  const int64_t t1 = min(t0 + chunk, total);
+  const int tpr = a.cap / Y::kTok;  // tiles per row (without counts)
+  __shared__ int live_pre[kLiveRows + 1];
+  __shared__ int live_wt[kWaves];
+  const bool by_count = a.counts != nullptr && rows <= kLiveRows;
+  int live_mine[kLivePer];
+  if (by_count) live_load(live_mine, a.counts, rows, a.cap, Y::kTok);  // in flight with the length loads below
   const int gcap = v.token_capacity / kGroup;
 
   // Segments k0..n-1 of this wave: rows that start and end inside the wave's range, so no
@@ -269,20 +327,39 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     len_tp[i] = tp;
     len_cur[i] = tp + min(max(v.tail_tokens[i], 0), v.tail_capacity);
   }
-  __syncthreads();
+  if (by_count) live_prefix(live_pre, live_wt, live_mine, rows);  // (its barriers also order the length cache)
+  else __syncthreads();
+  const int64_t total = by_count ? static_cast<int64_t>(__builtin_amdgcn_readfirstlane(live_pre[rows]))
+                                 : static_cast<int64_t>(rows) * tpr;
+  const int64_t chunk = uniform64((total + a.waves - 1) / a.waves);
+  const int64_t t0 = static_cast<int64_t>(w) * chunk;
+  const int64_t t1 = min(t0 + chunk, total);
 
   // Tile cursor: row, batch, tile within the row.  Cursors advance one tile at a time (an
   // integer division per tile would cost ~100 scalar instructions) and stop at the last
   // tile (tiles past the end are loaded again, never computed).
   struct Pos {
     int64_t i;
-    int bh, b, h, k;
+    int bh, b, h, k, kend;  // kend: live tiles of row bh
   };
   auto pos_at = [&](int64_t tile) {
     Pos p;
     p.i = tile;
-    p.bh = __builtin_amdgcn_readfirstlane(static_cast<int>(tile / tpr));
-    p.k = __builtin_amdgcn_readfirstlane(static_cast<int>(tile - static_cast<int64_t>(p.bh) * tpr));
+    if (by_count) {
+      int lo = 0, hi = rows;  // live_pre[lo] <= tile < live_pre[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (live_pre[mid] <= tile) lo = mid;
+        else hi = mid;
+      }
+      p.bh = __builtin_amdgcn_readfirstlane(lo);
+      p.k = __builtin_amdgcn_readfirstlane(static_cast<int>(tile - live_pre[p.bh]));
+      p.kend = __builtin_amdgcn_readfirstlane(live_pre[p.bh + 1] - live_pre[p.bh]);
+    } else {
+      p.bh = __builtin_amdgcn_readfirstlane(static_cast<int>(tile / tpr));
+      p.k = __builtin_amdgcn_readfirstlane(static_cast<int>(tile - static_cast<int64_t>(p.bh) * tpr));
+      p.kend = tpr;
+    }
     p.b = __builtin_amdgcn_readfirstlane(p.bh / v.heads);
     p.h = p.bh - p.b * v.heads;
     return p;
@@ -290,13 +367,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   auto step = [&](Pos& p) {
     if (p.i + 1 >= t1) return;
     ++p.i;
-    if (++p.k == tpr) {
+    if (++p.k == p.kend) {
       p.k = 0;
       ++p.bh;
       if (++p.h == v.heads) {
         p.h = 0;
         ++p.b;
       }
+      if (by_count) p.kend = __builtin_amdgcn_readfirstlane(live_pre[p.bh + 1] - live_pre[p.bh]);
     }
   };
 
@@ -699,13 +777,39 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 
 // Merge of row bh: slots [f+bh, l+bh] of each partial set (see gather_slot).
 __global__ __launch_bounds__(kMergeThreads) void gather_merge_kernel(const float* ws, int waves, int tpr, int nrows,
+                                                                     const int32_t* counts, int cap, int tok,
                                                                      float* out, int mode, const float* mass,
                                                                      const float* src, float* src_out) {
   __shared__ MergeLdsBuf S;
+  __shared__ int live_red[2][kMergeThreads / kWave];
   const int bh = blockIdx.x, tid = threadIdx.x;
-  const int64_t total = static_cast<int64_t>(nrows) * tpr;
+  // the row's live-tile range [rs, re) and the total, as the reader derived them
+  int64_t rs = static_cast<int64_t>(bh) * tpr, re = rs + tpr, total = static_cast<int64_t>(nrows) * tpr;
+  if (counts != nullptr && nrows <= kLiveRows) {
+    int before = 0, all = 0;
+    for (int r = tid; r < nrows; r += kMergeThreads) {
+      const int n = live_tiles(counts, r, cap, tok);
+      all += n;
+      if (r < bh) before += n;
+    }
+    before = wave_sum_int(before);
+    all = wave_sum_int(all);
+    if ((tid & 63) == 0) {
+      live_red[0][tid >> 6] = before;
+      live_red[1][tid >> 6] = all;
+    }
+    __syncthreads();
+    before = all = 0;
+    for (int w = 0; w < kMergeThreads / kWave; ++w) {
+      before += live_red[0][w];
+      all += live_red[1][w];
+    }
+    rs = before;
+    re = before + live_tiles(counts, bh, cap, tok);
+    total = all;
+  }
   const int64_t chunk = (total + waves - 1) / waves * kWaves;  // tiles per reader workgroup
-  const int64_t f = static_cast<int64_t>(bh) * tpr / chunk, l = (static_cast<int64_t>(bh + 1) * tpr - 1) / chunk;
+  const int64_t f = rs / chunk, l = (re - 1) / chunk;
   const int64_t o = static_cast<int64_t>(bh) * kDim + tid;
   const MergeParts P{ws + (f + bh) * kPartial, static_cast<int>(l - f + 1), nullptr};
   if (mode == kMergeSum) {
@@ -824,7 +928,7 @@ void launch_gather(GatherArgs& a, int rows, hipStream_t st) {
   }
   const int mode = MODE == kSelectedPV ? kMergeSum : (MODE == kSparseDelta ? kMergeMassDelta : kMergeMassDeltaFused);
   hipLaunchKernelGGL(gather_merge_kernel, dim3(rows), dim3(kMergeThreads), 0, st, static_cast<const float*>(a.ws),
-                     a.waves, a.tpr, rows, a.out, mode, a.mass, a.src, a.src_out);
+                     a.waves, a.tpr, rows, a.counts, a.cap, Lay<kLpt>::kTok, a.out, mode, a.mass, a.src, a.src_out);
 }
 
 }  // namespace
@@ -846,7 +950,7 @@ float* gather_partials(void* workspace, int rows) {
 
 extern "C" int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop, const int32_t* indices,
                                          const uint8_t* valid, const float* weights, int32_t capacity,
-                                         const uint16_t* v_cur, float* out, void* workspace, size_t workspace_bytes,
+                                         const int32_t* counts, const uint16_t* v_cur, float* out, void* workspace, size_t workspace_bytes,
                                          void* stream) {
   using namespace fl;
   clear_error();
@@ -863,6 +967,7 @@ extern "C" int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop
   a.valid = valid;
   a.weights = weights;
   a.cap = capacity;
+  a.counts = counts;
   a.ws = gather_partials(workspace, rows);
   a.out = out;
   launch_gather<kSelectedPV>(a, rows, static_cast<hipStream_t>(stream));
@@ -872,7 +977,8 @@ extern "C" int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop
 
 extern "C" int32_t fl_decode_attn_sparse_delta(const fl_cache_view* view, int32_t loop, const uint16_t* q,
                                                const uint16_t* k_cur, const uint16_t* v_cur, const int32_t* indices,
-                                               const uint8_t* valid, int32_t capacity, const float* source_output,
+                                               const uint8_t* valid, int32_t capacity, const int32_t* counts,
+                                               const float* source_output,
                                                const float* mass, float scaling, float* out, void* workspace,
                                                size_t workspace_bytes, void* stream) {
   using namespace fl;
@@ -892,6 +998,7 @@ extern "C" int32_t fl_decode_attn_sparse_delta(const fl_cache_view* view, int32_
   a.idx = indices;
   a.valid = valid;
   a.cap = capacity;
+  a.counts = counts;
   a.scaling = scaling;
   a.ws = gather_partials(workspace, rows);
   a.out = out;
@@ -906,7 +1013,8 @@ extern "C" int32_t fl_decode_attn_sparse_delta_fused(const fl_cache_view* view, 
                                                      const uint16_t* k_cur, const uint16_t* v_cur,
                                                      const int32_t* indices, const uint8_t* valid,
                                                      const float* source_weights, const uint16_t* source_v_cur,
-                                                     int32_t capacity, const float* mass, float scaling,
+                                                     int32_t capacity, const int32_t* counts, const float* mass,
+                                                     float scaling,
                                                      float* source_output, float* out, void* workspace,
                                                      size_t workspace_bytes, void* stream) {
   using namespace fl;
@@ -931,6 +1039,7 @@ extern "C" int32_t fl_decode_attn_sparse_delta_fused(const fl_cache_view* view, 
   a.weights = source_weights;
   a.vc1 = source_v_cur;
   a.cap = capacity;
+  a.counts = counts;
   a.scaling = scaling;
   a.ws = gather_partials(workspace, rows);
   a.out = out;

@@ -82,6 +82,7 @@ class _LayerSource:
     selected_weights: torch.Tensor
     current_value: torch.Tensor
     selected_output: torch.Tensor | None = None
+    counts: torch.Tensor | None = None  # selected slots per row (the sparse readers skip the padding)
 
 
 def _budget(tokens: int, fraction: float) -> int:
@@ -453,27 +454,27 @@ class FlashLoopEngine:
                 lc = cache.layers[li]
                 if loop < 2 or not sparse:
                     if loop == 1 and sparse:  # read, merge and loop-2 selection: two launches
-                        out, lg, (idx, valid, mass, sw, _) = lc.dense_source_attention_select(
+                        out, lg, (idx, valid, mass, sw, cnt) = lc.dense_source_attention_select(
                             loop, query=q, current_key=k, current_value=v, scaling=a.scaling, fraction=fraction)
                     else:
                         out, _ = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
                                                            scaling=a.scaling, return_logits=False)
                     projected = kernels.gemv(out.reshape(bsz, -1), [w["o"]])
                     if loop == 1 and sparse:
-                        sources[li] = _LayerSource(projected, idx, valid, mass, sw, v)
+                        sources[li] = _LayerSource(projected, idx, valid, mass, sw, v, counts=cnt)
                 else:
                     src = sources[li]
                     if src.selected_output is None:
                         delta, so = lc.cached_mass_sparse_attention_delta_with_source(
                             loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
                             source_weights=src.selected_weights, source_current_value=src.current_value,
-                            global_mass=src.global_mass, scaling=a.scaling)
+                            global_mass=src.global_mass, scaling=a.scaling, counts=src.counts)
                         src.selected_output = so
                     else:
                         delta = lc.cached_mass_sparse_attention_delta(
                             loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
                             source_selected_output=src.selected_output, global_mass=src.global_mass,
-                            scaling=a.scaling)
+                            scaling=a.scaling, counts=src.counts)
                     projected = kernels.gemv(delta.reshape(bsz, -1), [w["o"]], epilogue=kernels.EPI_ADD,
                                              addend=src.projected_output)
                 pending = dict(x=projected, w_a=w["ln2"], w_b=w["ln3"])
@@ -514,27 +515,27 @@ class FlashLoopEngine:
                 lc = cache.layers[li]
                 if loop < 2 or not sparse:
                     if loop == 1 and sparse:
-                        out, lg, (idx, valid, mass, w, _) = lc.dense_source_attention_select(
+                        out, lg, (idx, valid, mass, w, cnt) = lc.dense_source_attention_select(
                             loop, query=q, current_key=k, current_value=v, scaling=a.scaling, fraction=fraction)
                     else:
                         out, _ = lc.dense_source_attention(loop, query=q, current_key=k, current_value=v,
                                                            scaling=a.scaling, return_logits=False)
                     projected = a.o_proj(out.to(q.dtype).transpose(1, 2).reshape(bsz, 1, -1))
                     if loop == 1 and sparse:
-                        sources[li] = _LayerSource(projected, idx, valid, mass, w, v)
+                        sources[li] = _LayerSource(projected, idx, valid, mass, w, v, counts=cnt)
                 else:
                     src = sources[li]
                     if src.selected_output is None:
                         delta, so = lc.cached_mass_sparse_attention_delta_with_source(
                             loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
                             source_weights=src.selected_weights, source_current_value=src.current_value,
-                            global_mass=src.global_mass, scaling=a.scaling)
+                            global_mass=src.global_mass, scaling=a.scaling, counts=src.counts)
                         src.selected_output = so
                     else:
                         delta = lc.cached_mass_sparse_attention_delta(
                             loop, query=q, current_key=k, current_value=v, indices=src.indices, valid=src.valid,
                             source_selected_output=src.selected_output, global_mass=src.global_mass,
-                            scaling=a.scaling)
+                            scaling=a.scaling, counts=src.counts)
                     projected = src.projected_output + a.o_proj(
                         delta.to(v.dtype).transpose(1, 2).reshape(bsz, 1, -1))
                 h = residual + layer.input_layernorm_2(projected)

@@ -205,9 +205,20 @@ def decode_topk(logits: torch.Tensor, n_keys: torch.Tensor, fraction: float, cap
     return idx, valid, mass, w, counts
 
 
+def _counts_ptr(counts, rows):
+    """Device pointer of the optional per-row selected counts (i32 [rows]) or None."""
+    if counts is None:
+        return None
+    counts = counts.reshape(rows)
+    _require(counts, torch.int32, "counts")
+    return counts.data_ptr()
+
+
 def fused_cross_loop_pv(view, loop, indices, valid, weights, current_value, *, device,
-                        workspace: Workspace | None = None):
-    """``pv_cross_loop_cuda`` + current-token term replacement (engine.py:346-371)."""
+                        workspace: Workspace | None = None, counts=None):
+    """``pv_cross_loop_cuda`` + current-token term replacement (engine.py:346-371).
+    ``counts``: optional i32 ``[B*H]`` selected slots per row (every valid slot of row r
+    lies below counts[r], as the top-k writes them): the reader then skips the padding."""
     lib = load()
     rows = view.batch * view.heads
     cap = indices.shape[-1]
@@ -221,15 +232,17 @@ def fused_cross_loop_pv(view, loop, indices, valid, weights, current_value, *, d
     out = torch.empty(rows, HEAD_DIM, dtype=torch.float32, device=device)
     ws = (workspace or _WS).get(lib.fl_decode_selected_workspace(C.byref(view), cap), device)
     rc = lib.fl_decode_selected_pv(C.byref(view), loop, indices.data_ptr(), valid.data_ptr(), weights.data_ptr(),
-                                   cap, vc.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
+                                   cap, _counts_ptr(counts, rows), vc.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                   ws.numel(), _stream())
     check(rc, "fl_decode_selected_pv")
     return out
 
 
 def fused_sparse_attention_delta(view, loop, query, current_key, current_value, indices, valid,
                                  source_selected_output, global_mass, scaling, *, device,
-                                 workspace: Workspace | None = None):
-    """``sparse_attention_delta_cuda`` replacement -> delta f32 [B*H,128]."""
+                                 workspace: Workspace | None = None, counts=None):
+    """``sparse_attention_delta_cuda`` replacement -> delta f32 [B*H,128] (``counts`` as
+    in ``fused_cross_loop_pv``)."""
     lib = load()
     rows = view.batch * view.heads
     cap = indices.shape[-1]
@@ -245,7 +258,8 @@ def fused_sparse_attention_delta(view, loop, query, current_key, current_value, 
     out = torch.empty(rows, HEAD_DIM, dtype=torch.float32, device=device)
     ws = (workspace or _WS).get(lib.fl_decode_selected_workspace(C.byref(view), cap), device)
     rc = lib.fl_decode_attn_sparse_delta(C.byref(view), loop, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                         indices.data_ptr(), valid.data_ptr(), cap, src.data_ptr(),
+                                         indices.data_ptr(), valid.data_ptr(), cap, _counts_ptr(counts, rows),
+                                         src.data_ptr(),
                                          mass.data_ptr(), float(scaling), out.data_ptr(), ws.data_ptr(),
                                          ws.numel(), _stream())
     check(rc, "fl_decode_attn_sparse_delta")
@@ -254,9 +268,10 @@ def fused_sparse_attention_delta(view, loop, query, current_key, current_value, 
 
 def fused_sparse_attention_delta_with_source(view, loop, query, current_key, current_value, indices, valid,
                                              source_weights, source_current_value, global_mass, scaling, *,
-                                             device, workspace: Workspace | None = None):
+                                             device, workspace: Workspace | None = None, counts=None):
     """Loop-3/4 cached-mass delta that also forms the loop-2 selected aggregate from the
-    rows it reads.  Returns (delta f32 [B*H,128], source_output f32 [B*H,128])."""
+    rows it reads.  Returns (delta f32 [B*H,128], source_output f32 [B*H,128])
+    (``counts`` as in ``fused_cross_loop_pv``)."""
     lib = load()
     rows = view.batch * view.heads
     cap = indices.shape[-1]
@@ -276,7 +291,8 @@ def fused_sparse_attention_delta_with_source(view, loop, query, current_key, cur
     ws = (workspace or _WS).get(lib.fl_decode_selected_workspace(C.byref(view), cap), device)
     rc = lib.fl_decode_attn_sparse_delta_fused(C.byref(view), loop, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
                                                indices.data_ptr(), valid.data_ptr(), weights.data_ptr(),
-                                               vc1.data_ptr(), cap, mass.data_ptr(), float(scaling),
+                                               vc1.data_ptr(), cap, _counts_ptr(counts, rows), mass.data_ptr(),
+                                               float(scaling),
                                                src.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), _stream())
     check(rc, "fl_decode_attn_sparse_delta_fused")
     return out, src

@@ -261,6 +261,12 @@ int32_t fl_decode_attn_dense_select(const fl_cache_view* view, int32_t loop,
  *   out[bh] = sum_j valid*weights[bh,j] * V_loop[indices[bh,j]],
  * where index packed_tokens[b]+tail_tokens[b] is the current token (v_cur).
  * indices/valid/weights: [B*H, capacity].  out f32 [B*H, 128].
+ * counts (nullable) i32 [B*H]: row r's valid slots all lie below counts[r] (clamped to
+ * [0, capacity]; slots at or past it are not read), as fl_decode_topk writes them.  The
+ * readers then partition only the slots below each row's count, so a ragged batch's
+ * padding costs nothing; null = every row holds `capacity` slots.  The reference passes
+ * no counts (its kernels also visit every padding slot); results are identical with or
+ * without them whenever the contract holds.
  * workspace: fl_decode_selected_workspace() bytes, with the same contract as
  * fl_decode_attn_dense.  The sparse readers (this call and the two below) address V
  * codes through the K line (the view's value_codes[s] must be key_codes[s] + 64, as
@@ -269,7 +275,7 @@ int32_t fl_decode_attn_dense_select(const fl_cache_view* view, int32_t loop,
 size_t fl_decode_selected_workspace(const fl_cache_view* view, int32_t capacity);
 int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop, const int32_t* indices,
                               const uint8_t* valid, const float* weights, int32_t capacity,
-                              const uint16_t* v_cur, float* out,
+                              const int32_t* counts, const uint16_t* v_cur, float* out,
                               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -280,13 +286,13 @@ int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop, const int
  * `CrossLoopKVLayer.cached_mass_sparse_attention_delta` (flashloop/cache.py:1517-1617):
  *   delta = mass * (softmax_S(scaling*q.K_loop[S]) . V_loop[S] - source_output)
  * over the valid selected indices S (the current token handled as in
- * fl_decode_selected_pv, with k_cur/v_cur).  source_output f32 [B*H,128],
- * mass f32 [B*H], out f32 [B*H,128].
+ * fl_decode_selected_pv, with k_cur/v_cur; counts as there).  source_output f32
+ * [B*H,128], mass f32 [B*H], out f32 [B*H,128].
  */
 int32_t fl_decode_attn_sparse_delta(const fl_cache_view* view, int32_t loop,
                                     const uint16_t* q, const uint16_t* k_cur,
                                     const uint16_t* v_cur, const int32_t* indices,
-                                    const uint8_t* valid, int32_t capacity,
+                                    const uint8_t* valid, int32_t capacity, const int32_t* counts,
                                     const float* source_output, const float* mass,
                                     float scaling, float* out,
                                     void* workspace, size_t workspace_bytes, void* stream);
@@ -306,7 +312,7 @@ int32_t fl_decode_attn_sparse_delta_fused(const fl_cache_view* view, int32_t loo
                                           const uint16_t* v_cur, const int32_t* indices,
                                           const uint8_t* valid, const float* source_weights,
                                           const uint16_t* source_v_cur, int32_t capacity,
-                                          const float* mass, float scaling, float* source_output,
+                                          const int32_t* counts, const float* mass, float scaling, float* source_output,
                                           float* out, void* workspace, size_t workspace_bytes,
                                           void* stream);
 

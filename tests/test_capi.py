@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 @pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
 def test_argument_errors_are_reported_without_launching():
     lib = _lib.load()
-    assert lib.fl_abi_version() == 3
+    assert lib.fl_abi_version() == 4
     rc = lib.fl_decode_topk(None, 1, 1, None, 1, 0.1, 64, None, None, None, None, None, None, None)
     assert rc == _lib.FL_E_INVALID
     assert b"null" in lib.fl_last_error()
@@ -95,8 +95,8 @@ def test_sparse_readers_require_value_codes_in_the_key_lines():
 
     def call(value_codes):
         v.value_codes[0] = value_codes
-        return lib.fl_decode_selected_pv(C.byref(v), 0, 0x5000, 0x6000, 0x7000, 16, 0x8000, 0x9000, 0x100000, 0,
-                                         None)
+        return lib.fl_decode_selected_pv(C.byref(v), 0, 0x5000, 0x6000, 0x7000, 16, None, 0x8000, 0x9000, 0x100000,
+                                         0, None)
 
     assert call(0x20000) == _lib.FL_E_INVALID and b"second half" in lib.fl_last_error()
     # the laid-out view passes this check and stops at the next one (the workspace size)
