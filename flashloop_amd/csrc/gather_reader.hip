@@ -142,7 +142,8 @@ __device__ __forceinline__ float dot_bf16_words(uint4 w, const float* q) {
 // ---------------------------------------------------------------------------------
 // Persistent tile readers.  The selection of row bh is cut into tiles of T slots; wave
 // w of the grid owns tiles [w*chunk, min((w+1)*chunk, total)) of the row-major tile
-// sequence (chunk = ceil(total / waves)) and runs them one after another: a tile issues
+// sequence (chunk = ceil(total / waves); the sequence holds only each row's live tiles
+// when counts are given) and runs them one after another: a tile issues
 // all its loads at once (index, then rank rows / codes / metadata) and many resident
 // waves per CU overlap each other's load latencies.  Inside a tile LPT lanes own one
 // slot (lane = LPT*n + part, 128/LPT channels per lane, T = 64/LPT slots).  The four

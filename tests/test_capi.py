@@ -23,6 +23,31 @@ def test_header_declares_the_bound_signatures():
     assert _declared_functions() == sorted(_lib.SIGNATURES)
 
 
+def test_header_parameter_counts_match_the_bindings():
+    """Every declaration's parameter count equals its ctypes binding's: a parameter added
+    on one side only (as the sparse readers' counts were) shifts every later argument."""
+    text = (ROOT / "include" / "flashloop_amd.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    for name, params in re.findall(r"\b(fl_[a-z0-9_]+)\s*\(([^;]*?)\)\s*;", text):
+        params = " ".join(params.split())
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert n == len(_lib.SIGNATURES[name][1]), f"{name}: header {n} parameters, binding {len(_lib.SIGNATURES[name][1])}"
+
+
+def test_sparse_reader_counts_only_for_ragged_batches():
+    """The layer hands the selection's counts to the sparse readers only when its
+    sequences differ in length (equal lengths leave no padding to skip)."""
+    from flashloop_amd.cache import CrossLoopKVLayer, LayerGeometry
+
+    layer = CrossLoopKVLayer(LayerGeometry(2, 1, 256, 128, (256, 256, 1, 1)), "cpu")
+    counts = object()
+    layer.packed_host, layer.tail_host = [192, 128], [70, 134]  # 262 keys each
+    assert layer._reader_counts(counts) is None
+    layer.tail_host = [70, 100]
+    assert layer._reader_counts(counts) is counts
+    assert layer._reader_counts(None) is None
+
+
 @pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
 def test_library_exports_every_declared_symbol():
     lib = C.CDLL(str(_lib.LIB_PATH))
