@@ -41,6 +41,17 @@ struct DenseArgs {
   int waves;  // persistent waves in the grid
 };
 
+// Combine row bh's partials (dense_merge_row).  `pieces` loops were read by one launch
+// (dense_pair_kernel: 2): block p*BH + bh merges row bh of piece p.  Defined ahead of the
+// reader kernels: with its code placed after them in the code object, the same
+// instructions ran 0.8 us longer per launch (cfg3, measured in one process).
+__global__ __launch_bounds__(kMergeThreads) void dense_merge_kernel(const float* ws0, const float* ws1, int W,
+                                                                    fl_cache_view v, float* out0, float* out1,
+                                                                    int pieces) {
+  __shared__ DenseMergeLds S;
+  dense_merge_row(S, blockIdx.x, ws0, ws1, W, v, out0, out1, pieces);
+}
+
 // Position in the work sequence: row (b, h), group gi of gb, row's first unit vs.
 struct Cursor {
   int b, h, gi, gb;
@@ -301,7 +312,7 @@ __device__ __forceinline__ void compute_group(const GroupSet<NS>& gs, WaveState&
 
   // ---- softmax of the lane's own token (row = lane: tile `quarter`, position n)
   const float lgo = quarter == 0 ? lg[0] : quarter == 1 ? lg[1] : quarter == 2 ? lg[2] : lg[3];
-  if (LOGITS) lgbuf[lane] = lgo;  // staged; written out in batches (see flush_logits)
+  if (LOGITS) lgbuf[lane] = lgo;  // staged; written out in batches (stage_flush)
   // the wave's maximum is formed only when some token exceeds m by more than e^8
   if (__ballot(lgo > st.m + kLazyRescale)) {  // wave-uniform
     const float gmax = wave_max(lgo);
@@ -527,7 +538,12 @@ __device__ __forceinline__ void stage_flush(const DenseArgs& a, const SegMeta* s
       // a row never writes past its stride (device lengths above the host maxima)
       const int64_t room = a.logits_stride - static_cast<int64_t>(m.gi0) * kGroup;
       const int cnt = static_cast<int>(min(static_cast<int64_t>(m.count * kGroup), max(room, int64_t{0})));
-      for (int e = lane; e < cnt; e += kWave) dst[e] = src[e];
+      // 16 bytes per lane and store (a row's logits start on a 256-byte boundary of the
+      // group grid; the stride may leave a row 4-byte aligned only: then dword stores)
+      const int c4 = (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 ? cnt >> 2 : 0;
+      for (int e = lane; e < c4; e += kWave)
+        reinterpret_cast<float4*>(dst)[e] = reinterpret_cast<const float4*>(src)[e];
+      for (int e = 4 * c4 + lane; e < cnt; e += kWave) dst[e] = src[e];
     }
     if (!(last_open && k == n - 1)) {
       float* part = a.ws + partial_slot(w, m.bh) * kPartial;
@@ -711,14 +727,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
   dense_range<2, true>(a1, mine.l2, rl, w, max(u0, U) - U, max(u1, U) - U);
 }
 
-// Combine row bh's partials (dense_merge_row).  `pieces` loops were read by one launch
-// (dense_pair_kernel: 2): block p*BH + bh merges row bh of piece p.
-__global__ __launch_bounds__(kMergeThreads) void dense_merge_kernel(const float* ws0, const float* ws1, int W,
-                                                                    fl_cache_view v, float* out0, float* out1,
-                                                                    int pieces) {
-  __shared__ DenseMergeLds S;
-  dense_merge_row(S, blockIdx.x, ws0, ws1, W, v, out0, out1, pieces);
-}
 
 int cu_count() {
   static std::mutex mu;
