@@ -450,7 +450,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      // row base (scalar) + line offset (32-bit: row < row_capacity < 2^24)
+      // row base (scalar) + line offset (32-bit: row < row_capacity <= 2^24, checked on the host)
       const int64_t base = static_cast<int64_t>(sl.bh) * v.row_capacity[s] * kCodeStride;
       const uint32_t off = static_cast<uint32_t>(row[s]) * kCodeStride + 4 * kWords * part;
       if (kSoftmax) load_words<LPT>(T.kw[s], v.key_codes[s] + base + off);
@@ -833,6 +833,8 @@ __global__ __launch_bounds__(kMergeThreads) void gather_merge_kernel(const float
   if (tid < kDim) out[o] = res;
 }
 
+constexpr int32_t kMaxGatherRows = 1 << 24;  // rows per (b, h) and stream that 32-bit line offsets address
+
 int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t* indices, const uint8_t* valid,
                           int32_t capacity, void* workspace, size_t workspace_bytes, size_t need, const char* who) {
   FL_REQUIRE(view != nullptr, std::string(who) + ": view is null");
@@ -846,10 +848,14 @@ int32_t check_gather_args(const fl_cache_view* view, int32_t loop, const int32_t
   // the readers load row 0 of every stream (and token 0's records) in place of a slot that
   // is absent there, so these must exist even when no prefix is packed yet
   FL_REQUIRE(v.token_capacity > 0 && v.value_meta_token, std::string(who) + ": no token records");
+  // a selected row's code line and token record are addressed by 32-bit offsets from the
+  // (b, h) row's base: row * 128 and token * 64 bytes
+  FL_REQUIRE(v.token_capacity <= kMaxGatherRows, std::string(who) + ": token_capacity above 2^24 tokens per row");
   for (int s = 0; s <= loop; ++s) {
     FL_REQUIRE(v.key_codes[s] && v.key_meta[s] && v.value_codes[s] && v.value_meta[s] && v.key_meta_half[s],
                std::string(who) + ": null stream pointer");
     FL_REQUIRE(v.row_capacity[s] > 0, std::string(who) + ": stream without rows");
+    FL_REQUIRE(v.row_capacity[s] <= kMaxGatherRows, std::string(who) + ": row_capacity above 2^24 rows per stream");
     if (s >= 2) FL_REQUIRE(v.rank[s - 2] != nullptr, std::string(who) + ": null rank map");
     FL_REQUIRE(v.value_codes[s] == v.key_codes[s] + kCodeStride / 2,
                std::string(who) + ": value_codes must be the second half of key_codes' lines");

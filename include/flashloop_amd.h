@@ -270,7 +270,8 @@ int32_t fl_decode_attn_dense_select(const fl_cache_view* view, int32_t loop,
  * workspace: fl_decode_selected_workspace() bytes, with the same contract as
  * fl_decode_attn_dense.  The sparse readers (this call and the two below) address V
  * codes through the K line (the view's value_codes[s] must be key_codes[s] + 64, as
- * laid out above; FL_E_INVALID otherwise).
+ * laid out above; FL_E_INVALID otherwise), and they take token_capacity and every
+ * row_capacity[s] up to 2^24 (32-bit line offsets within a (b,h) row; FL_E_INVALID above).
  */
 size_t fl_decode_selected_workspace(const fl_cache_view* view, int32_t capacity);
 int32_t fl_decode_selected_pv(const fl_cache_view* view, int32_t loop, const int32_t* indices,

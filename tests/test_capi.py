@@ -137,6 +137,13 @@ def test_sparse_readers_require_value_codes_in_the_key_lines():
     v.key_meta_half[0] = 0x4000
     v.value_meta_token = 0
     assert call(0x10000 + 64) == _lib.FL_E_INVALID and b"token records" in lib.fl_last_error()
+    # rows and tokens beyond what the readers' 32-bit line offsets address are refused
+    v.value_meta_token = 0x1200
+    v.token_capacity = (1 << 24) + 64
+    assert call(0x10000 + 64) == _lib.FL_E_INVALID and b"token_capacity above" in lib.fl_last_error()
+    v.token_capacity = 64
+    v.row_capacity[0] = (1 << 24) + 1
+    assert call(0x10000 + 64) == _lib.FL_E_INVALID and b"row_capacity above" in lib.fl_last_error()
 
 
 @pytest.mark.skipif(not _lib.LIB_PATH.exists(), reason="library not built")
