@@ -133,6 +133,36 @@ def restated_dense_logits(layer, loop: int, rows, q, k_cur, scaling: float) -> l
     return out
 
 
+def restated_selected_aggregate(layer, rows, indices, valid, weights, v_cur) -> np.ndarray:
+    """fp64 loop-2 selected aggregate ``sum_j w_j V[t_j]`` of the sparse readers' own
+    arithmetic for the (b,h) rows ``rows``: a prefix token's V is
+    ``sum_{s<=1} code_s * scale_s + min_s`` from the packed codes and the fp32 per-token
+    metadata, with no bf16 rounding between the streams; tail rows and the current token
+    are the raw BF16 rows.  ``indices``/``valid``/``weights``: ``[len(rows), cap]``;
+    ``v_cur``: ``[len(rows), 128]``."""
+    out = []
+    heads = layer.heads
+    for i, r in enumerate(rows):
+        b = r // heads
+        tp, tl = layer.packed_host[b], layer.tail_host[b]
+        acc = np.zeros(128, np.float64)
+        for j in np.nonzero(valid[i])[0]:
+            t, wt = int(indices[i, j]), float(weights[i, j])
+            if t < tp:
+                v = np.zeros(128, np.float64)
+                for s in range(2):
+                    codes = unpack_codes(layer.value_codes[s][r, t]).astype(np.float64)  # [128]
+                    meta = layer.value_meta[s][r, t].cpu().numpy().astype(np.float64)  # [half, (scale, min)]
+                    v += codes * np.repeat(meta[:, 0], 64) + np.repeat(meta[:, 1], 64)
+            elif t < tp + tl:
+                v = layer.tail_value[1][r, t - tp].float().cpu().numpy().astype(np.float64)
+            else:
+                v = np.asarray(v_cur[i], np.float64)
+            acc += wt * v
+        out.append(acc)
+    return np.stack(out)
+
+
 def step_vs_oracle_rows(got, rows, H, nk, nv, masks, q, kc, vc, scaling, fraction, what=""):
     """One decode step of a batch-one cache against the oracle at the head rows ``rows``.
 
