@@ -342,14 +342,21 @@ def _step_vs_oracle(w, layer, m3=None, m4=None, frac=0.10):
     cap = step.indices.shape[-1]
     sel = OA.decode_topk(rows_lg, frac, kpad=cap)
     assert np.array_equal(step.indices.cpu().numpy().reshape(R, cap), sel.indices), "selected indices differ"
-    # end-to-end selection overlap against the oracle's own logits (reported, not bit-exact)
+    # end-to-end selection overlap against the oracle's own logits (reported, not bit-exact:
+    # the kernel's logits differ from the bf16-chain oracle's by ~1e-3, which can swap keys
+    # at a row's boundary).  One swap costs a row 1/k of its overlap, so the bound is per
+    # row in swaps (at most 2, or 2% of k) and pooled over rows (> 99% once the rows
+    # select 500 keys or more); measured pooled overlap >= 99.45% in every parity case.
     sel_o = OA.decode_topk(lg1, frac, kpad=cap)
-    overlap = np.mean([
-        len(set(sel.indices[r, : sel.count[r]]) & set(sel_o.indices[r, : sel_o.count[r]])) / sel_o.count[r]
-        for r in range(R)
-    ])
+    common = [len(set(sel.indices[r, : sel.count[r]]) & set(sel_o.indices[r, : sel_o.count[r]])) for r in range(R)]
+    total = int(np.sum(sel_o.count[:R]))
+    overlap = float(np.sum(common)) / total
     print(f"[parity] selection overlap with the oracle's own logits {overlap:.5f}", flush=True)
-    assert overlap > 0.99, f"selection overlap with oracle logits {overlap:.4f}"  # measured >= 0.9945
+    for r in range(R):
+        k = int(sel_o.count[r])
+        assert k - common[r] <= max(2, math.ceil(0.02 * k)), f"row {r}: {k - common[r]} of {k} keys differ"
+    if total >= 500:
+        assert overlap > 0.99, f"selection overlap with oracle logits {overlap:.4f}"
     # selected aggregate and cached-mass deltas, oracle run on the kernel's selection
     so = OA.selected_value_aggregate(sel.indices, sel.valid, sel.selected_weights, Vr[1], vc[1], lengths)
     assert_close(np32(step.selected_output).reshape(R, 128), so, what="selected output")
