@@ -41,6 +41,10 @@ __device__ __forceinline__ Quant make_quant(float mn, float mx, bool any) {
     mn = 0.0f;
     mx = 0.0f;
   }
+  // A group whose smallest value is a zero keeps +0 as its minimum (-0 + +0 = +0):
+  // which zero a min reduction returns over a mix of +0 and -0 depends on its
+  // evaluation order.  Reconstructions are the same either way.
+  mn = __fadd_rn(mn, 0.0f);
   const float span = __fsub_rn(mx, mn);
   const float scale = span > 0.0f ? __fdiv_rn(span, 15.0f) : 1.0f;
   return {scale, mn, __fdiv_rn(1.0f, scale)};

@@ -87,6 +87,10 @@ def asymmetric_fake_quant(values: np.ndarray, axis: int, active: np.ndarray | No
         any_active = act.any(axis=axis, keepdims=True)
         mn = np.where(any_active, mn, F32(0.0)).astype(F32)
         mx = np.where(any_active, mx, F32(0.0)).astype(F32)
+    # A zero minimum is stored as +0 (-0 + 0 = +0): torch's amin returns either zero
+    # over a mix of +0 and -0, depending on its evaluation order.  The codes and the
+    # reconstruction do not depend on that sign.
+    mn = (mn + F32(0.0)).astype(F32)
     span = (mx - mn).astype(F32)
     scale = np.where(span > 0, span / LEVELS, F32(1.0)).astype(F32)
     q = np.rint((work - mn) / scale).astype(F32)  # np.rint: round half to even

@@ -32,7 +32,7 @@ def oracle_prefix(keys, values, m3=None, m4=None):
 
 
 def assert_layer_matches_chain(layer, chain, tp, batch, heads, row_ids=None):
-    """Bit-exact codes, K/V metadata of all four streams against the oracle chain.
+    """Bit-exact codes, K/V metadata (compared as bit patterns, so the sign of a zero counts) of all four streams against the oracle chain.
     ``row_ids``: the layer's (b,h) rows of the chain's rows (default: the same rows)."""
     bh = batch * heads
     ids = np.arange(bh) if row_ids is None else np.asarray(row_ids)
@@ -45,8 +45,8 @@ def assert_layer_matches_chain(layer, chain, tp, batch, heads, row_ids=None):
         vmeta = layer.value_meta[s].cpu().numpy()
         ks = sc.k_scale.reshape(bh, G, 128)
         km = sc.k_min.reshape(bh, G, 128)
-        assert np.array_equal(kmeta[ids, :G, :, 0], ks), f"stream {s}: K scale mismatch"
-        assert np.array_equal(kmeta[ids, :G, :, 1], km), f"stream {s}: K min mismatch"
+        assert np.array_equal(kmeta[ids, :G, :, 0].view(np.uint32), ks.view(np.uint32)), f"stream {s}: K scale mismatch"
+        assert np.array_equal(kmeta[ids, :G, :, 1].view(np.uint32), km.view(np.uint32)), f"stream {s}: K min mismatch"
         okc = sc.k_codes.reshape(batch, heads, tp, 128)
         ovc = sc.v_codes.reshape(batch, heads, tp, 128)
         ovs = sc.v_scale.reshape(batch, heads, tp, 2)
@@ -65,8 +65,8 @@ def assert_layer_matches_chain(layer, chain, tp, batch, heads, row_ids=None):
                 r = ids[b * heads + h]
                 assert np.array_equal(kc[r, rows], okc[b, h, t_idx]), f"stream {s}: K codes mismatch (b={b}, h={h})"
                 assert np.array_equal(vc[r, rows], ovc[b, h, t_idx]), f"stream {s}: V codes mismatch (b={b}, h={h})"
-                assert np.array_equal(vmeta[r, rows, :, 0], ovs[b, h, t_idx]), f"stream {s}: V scale mismatch"
-                assert np.array_equal(vmeta[r, rows, :, 1], ovm[b, h, t_idx]), f"stream {s}: V min mismatch"
+                assert np.array_equal(vmeta[r, rows, :, 0].view(np.uint32), ovs[b, h, t_idx].view(np.uint32)), f"stream {s}: V scale mismatch"
+                assert np.array_equal(vmeta[r, rows, :, 1].view(np.uint32), ovm[b, h, t_idx].view(np.uint32)), f"stream {s}: V min mismatch"
 
 
 def materialized(nk, nv, chain, tp):

@@ -875,6 +875,45 @@ def test_extreme_ranges_codec_and_half_copies():
     _assert_half_copies(layer, chain, tp, b, h)
 
 
+@pytest.mark.parametrize("masked", [False, True])
+def test_signed_zero_minima(masked):
+    """Groups whose smallest value is a zero, as +0, -0 or a mix of both (sparse data
+    gives -0 from x * 0 with x < 0): the stored minimum is +0 in every copy (fp32 and
+    fp16 K and V metadata, the per-token record), bit for bit with the oracle, and the
+    codes and reconstructions are bit-exact too."""
+    print(f"case: signed-zero minima B2 H2 T300 masked={masked}", flush=True)
+    b, h, t = 2, 2, 300
+    g = torch.Generator().manual_seed(31)
+    ks, vs = [], []
+    for r in range(4):
+        x = torch.randn(b, h, t, 128, generator=g).abs()
+        sign = torch.where(torch.rand(b, h, t, 128, generator=g) < 0.5, -1.0, 1.0)
+        keep = torch.rand(b, h, t, 128, generator=g) < 0.3
+        k = torch.where(keep, x, torch.zeros(()) * sign)  # >= 0 with +-0 zeros
+        k[0, 0] = torch.zeros(()) * sign[0, 0]  # whole row of +-0: K groups and V tokens all zero
+        k[1, 1, :, :64] = -0.0  # V halves of only -0
+        ks.append(k.bfloat16())
+        vs.append(k.flip(-2).bfloat16())
+    assert (torch.signbit(ks[0]) & (ks[0] == 0)).any()
+    kw, m3, m4 = {}, None, None
+    if masked:
+        m3, m4 = _masks(b, t, 31, p3=0.3, p4=0.5)
+        kw = dict(mask_loop3=torch.from_numpy(m3).to(DEV), mask_loop4=torch.from_numpy(m4).to(DEV))
+    layer = CrossLoopKVLayer.from_prefill([k.to(DEV) for k in ks], [v.to(DEV) for v in vs], recon=True, **kw)
+    torch.cuda.synchronize()
+    nk, nv, chain, tp = oracle_prefix(ks, vs, m3, m4)
+    assert_layer_matches_chain(layer, chain, tp, b, h)
+    for s_ in range(4):
+        km = chain.streams[s_].k_min
+        assert not np.signbit(km[km == 0]).any() and (km == 0).any()
+    for r in range(4):
+        got_k = np32(layer.recon_keys[r]).reshape(b, h, t, 128)[:, :, :tp]
+        got_v = np32(layer.recon_values[r]).reshape(b, h, t, 128)[:, :, :tp]
+        assert np.array_equal(got_k.view(np.uint32), chain.recon_keys[r].view(np.uint32)), f"R_{r} keys differ"
+        assert np.array_equal(got_v.view(np.uint32), chain.recon_values[r].view(np.uint32)), f"R_{r} values differ"
+    _assert_half_copies(layer, chain, tp, b, h)
+
+
 @pytest.mark.parametrize("n", [3000, 40000])
 def test_topk_signed_zeros_tie(n):
     """-0.0 and +0.0 are equal scores: their tie goes to the lower index, as in a stable

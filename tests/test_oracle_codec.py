@@ -35,6 +35,30 @@ def test_constant_group_scale_one_codes_zero():
     assert np.all(fq.codes == 0) and np.all(fq.recon == 0.75)
 
 
+def test_zero_minimum_is_positive_zero():
+    """A group whose smallest value is a zero stores +0 as its minimum, whether its
+    zeros are +0, -0 or a mix (numpy's and torch's min over a mix return either);
+    codes and reconstructions are those of a +0 minimum, and no reconstruction is -0."""
+    x = np.zeros((1, 1, 64, 128), F32)
+    x[0, 0, :, 0] = -0.0  # all -0
+    x[0, 0, ::2, 1] = -0.0  # mixed
+    x[0, 0, 1::3, 2] = -0.0
+    x[0, 0, 5, 2] = 2.0  # mixed zeros with one non-zero above them
+    x[0, 0, :, 3] = -0.0
+    x[0, 0, 7, 3] = -1.0  # a negative minimum keeps its value
+    fq, _ = codec.quantize_k_per_channel(x)
+    mn = fq.minimum.reshape(-1)
+    assert mn[3] == -1.0
+    zero = mn == 0
+    assert zero[[0, 1, 2]].all() and not np.signbit(mn[zero]).any()
+    assert fq.scale.reshape(-1)[2] == F32(2.0) / F32(15)
+    assert fq.codes[0, 0, 5, 2] == 15 and fq.codes[0, 0, :5, 2].max() == 0
+    assert not np.signbit(fq.recon[fq.recon == 0]).any()
+    v = codec.quantize_v_per_token(np.where(np.arange(128) % 3 == 0, F32(-0.0), F32(0.0))[None, None, None, :]
+                                   * np.ones((1, 1, 4, 1), F32))
+    assert np.all(v.minimum == 0) and not np.signbit(v.minimum).any()
+
+
 def test_ramp_gives_codes_j():
     # per-channel ramp over 16 tokens repeated: min=-1, step 0.125 -> span 1.875, scale 0.125
     j = np.arange(64) % 16
