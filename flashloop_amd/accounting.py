@@ -9,6 +9,11 @@ fp16 copies of the metadata (the fp32 values are the stored codec state):
 * BF16 tail: ``tl * 128 * 2`` each for K and V; vectors q/k_cur/v_cur ``3 * 256``;
   output ``128 * 4``; logits (loop 2) ``(T+1) * 4``;
 * top-k: logits read ``(T+1) * 4`` + indices/valid/weights written ``cap * 9`` + mass;
+* pack (cache build, J1): reads the bf16 K and V of every loop, ``Tp * 4 * 2 * 256``
+  (plus, with loop-3/4 masks, one mask byte and one int32 rank per token and masked
+  loop of each sequence); writes per stream and stored row K and V codes ``2 * 64``,
+  V (scale, min) in fp32 and fp16 ``2 * (8 + 4)`` and the per-token record ``2 * 8``,
+  and per 64-token group K (scale, min) in fp32 and fp16 ``128 * (8 + 4)``;
 * sparse readers: per selected prefix row and stream, K codes 64 + V codes 64 +
   V metadata 16, plus 512 B of K metadata per touched (group, stream) -- these readers
   stream the fp16 copy of the K metadata; selected tail or current rows 256 per K or V;
@@ -36,6 +41,21 @@ def dense_bytes(packed, tail, streams: int, logits: bool) -> int:
     if logits:
         tot = tot + (p + t + 1) * 4
     return int(tot.sum())
+
+
+def pack_bytes(packed, stream_rows, masked_tokens: int = 0) -> tuple[int, int]:
+    """(read, written) algorithmic bytes of one cache build: ``packed`` = packed prefix
+    per (b,h) row, ``stream_rows[s]`` = rows stored in stream s per (b,h) row (the
+    packed prefix for loops 1/2, the active tokens for loops 3/4), ``masked_tokens`` =
+    tokens x masked loops summed over sequences (mask byte + rank entry each)."""
+    p = np.asarray(packed, np.int64)
+    read = int((p * 4 * 2 * BF16_ROW).sum()) + masked_tokens * (1 + 4)
+    written = 0
+    for rows in stream_rows:
+        r = np.asarray(rows, np.int64)
+        written += int((r * (2 * CODE_ROW + 2 * (VMETA_ROW // 2 + VMETA_ROW_F16 // 2) + VMETA_ROW)).sum())
+        written += int(((p // 64) * (KMETA_GROUP + KMETA_GROUP_F16)).sum())
+    return read, written
 
 
 def topk_bytes(packed, tail, cap: int) -> int:

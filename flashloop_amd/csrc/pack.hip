@@ -63,6 +63,12 @@ __device__ __forceinline__ void round_bf16_pair(float& a, float& b) {
   b = __uint_as_float(w & 0xFFFF0000u);
 }
 
+// Two values that are already bf16 (their low 16 bits zero, as every reconstruction
+// here is after round_bf16_pair) as one packed bf16 pair: their upper halves.
+__device__ __forceinline__ uint32_t bf16_bits_pair(float lo, float hi) {
+  return (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u);
+}
+
 // code = clamp(rint((x - minimum) / scale), 0, 15).  The quotient is Markstein's
 // correction of a * RN(1/scale): with y = RN(1/b), q0 = RN(a*y) and the exact remainder
 // r = a - b*q0 (one fma), RN(q0 + r*y) is the correctly rounded a/b (P. Markstein,
@@ -76,8 +82,10 @@ constexpr float kMinFastScale = 0x1p-100f;
 
 __device__ __forceinline__ bool needs_exact_div(Quant q) { return !(q.scale >= kMinFastScale); }
 
+// Returns the code as a float (an integer in [0, 15]): the decode takes it as it is,
+// with no conversion back from the integer.
 template <bool EXACT_DIV>
-__device__ __forceinline__ uint32_t encode(float x, Quant q) {
+__device__ __forceinline__ float encode(float x, Quant q) {
   const float a = __fsub_rn(x, q.minimum);
   float c;
   if constexpr (EXACT_DIV) {
@@ -87,13 +95,12 @@ __device__ __forceinline__ uint32_t encode(float x, Quant q) {
     const float r = __fmaf_rn(-q0, q.scale, a);
     c = rintf(__fmaf_rn(r, q.inv, q0));
   }
-  c = fminf(fmaxf(c, 0.0f), 15.0f);
-  return static_cast<uint32_t>(c);
+  return fminf(fmaxf(c, 0.0f), 15.0f);
 }
 
 // code * scale + minimum before its bf16 rounding (round_bf16_pair)
-__device__ __forceinline__ float decode_f32(uint32_t code, Quant q) {
-  return __fadd_rn(__fmul_rn(static_cast<float>(code), q.scale), q.minimum);
+__device__ __forceinline__ float decode_f32(float code, Quant q) {
+  return __fadd_rn(__fmul_rn(code, q.scale), q.minimum);
 }
 
 // Raw buffer over `bytes` bytes at p (wave-uniform).  Loads past the end, or from a
@@ -171,8 +178,9 @@ __device__ __forceinline__ void key_loop(const PackArgs& a, int b, int bh, int g
     load_k_words<R + 1>(w_next, a, src_base, pair, quarter);
     tin_next = token_load<R + 1>(a, b, g, src_row0, lane);
   }
-  // active tokens of this loop, one bit per token (lane i holds token i)
-  const uint64_t act = __ballot(token_active<R>(a, tin));
+  // active tokens of this loop, one bit per token (lane i holds token i); loops 1/2
+  // have every token of a packed group (a constant, so the per-element tests fold away)
+  const uint64_t act = R < 2 ? ~0ull : __ballot(token_active<R>(a, tin));
   float x0[16], x1[16];
   float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY;
 #pragma unroll
@@ -218,10 +226,11 @@ __device__ __forceinline__ void key_loop(const PackArgs& a, int b, int bh, int g
       uint32_t c0 = 0, c1 = 0;
       float d0 = 0.0f, d1 = 0.0f;
       if ((act >> i) & 1) {
-        c0 = encode<EXACT>(x0[k], q0);
-        c1 = encode<EXACT>(x1[k], q1);
-        d0 = decode_f32(c0, q0);
-        d1 = decode_f32(c1, q1);
+        const float f0 = encode<EXACT>(x0[k], q0), f1 = encode<EXACT>(x1[k], q1);
+        c0 = static_cast<uint32_t>(f0);
+        c1 = static_cast<uint32_t>(f1);
+        d0 = decode_f32(f0, q0);
+        d1 = decode_f32(f1, q1);
         round_bf16_pair(d0, d1);
       }
       lds[i][pair & 15] = static_cast<uint8_t>(c0 | (c1 << 4));
@@ -234,15 +243,17 @@ __device__ __forceinline__ void key_loop(const PackArgs& a, int b, int bh, int g
         r1[k] = __fadd_rn(r1[k], d1);
         round_bf16_pair(r0[k], r1[k]);
       }
-      if (a.rk[R] != nullptr) {
-        const uint32_t packed = static_cast<uint32_t>(f32_to_bf16_rne(r0[k])) |
-                                (static_cast<uint32_t>(f32_to_bf16_rne(r1[k])) << 16);
-        *reinterpret_cast<uint32_t*>(a.rk[R] + src_base + static_cast<int64_t>(i) * kDim + 2 * pair) = packed;
-      }
     }
   };
   if (__builtin_expect(__any(needs_exact_div(q0) || needs_exact_div(q1)), 0)) encode_rows(std::true_type{});
   else encode_rows(std::false_type{});
+  // audit copy of the reconstruction (one branch, outside the encode loop)
+  if (a.rk[R] != nullptr) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      *reinterpret_cast<uint32_t*>(a.rk[R] + src_base + static_cast<int64_t>(quarter * 16 + k) * kDim + 2 * pair) =
+          bf16_bits_pair(r0[k], r1[k]);
+  }
   wave_lds_sync();
   const int row = token_row<R>(a, tin);
   const uint4 chunk = *reinterpret_cast<const uint4*>(lds[lane]);
@@ -325,10 +336,11 @@ __device__ __forceinline__ void value_loop(const PackArgs& a, int b, int bh, int
       uint32_t c0 = 0, c1 = 0;
       float d0 = 0.0f, d1 = 0.0f;
       if (act) {
-        c0 = encode<EXACT>(x[c], q);
-        c1 = encode<EXACT>(x[c + 1], q);
-        d0 = decode_f32(c0, q);
-        d1 = decode_f32(c1, q);
+        const float f0 = encode<EXACT>(x[c], q), f1 = encode<EXACT>(x[c + 1], q);
+        c0 = static_cast<uint32_t>(f0);
+        c1 = static_cast<uint32_t>(f1);
+        d0 = decode_f32(f0, q);
+        d1 = decode_f32(f1, q);
         round_bf16_pair(d0, d1);
       }
       words[c >> 3] |= (c0 | (c1 << 4)) << (4 * (c & 7));
@@ -365,8 +377,7 @@ __device__ __forceinline__ void value_loop(const PackArgs& a, int b, int bh, int
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        o[e] = static_cast<uint32_t>(f32_to_bf16_rne(rv[8 * k + 2 * e])) |
-               (static_cast<uint32_t>(f32_to_bf16_rne(rv[8 * k + 2 * e + 1])) << 16);
+        o[e] = bf16_bits_pair(rv[8 * k + 2 * e], rv[8 * k + 2 * e + 1]);
       }
       dst[k] = make_uint4(o[0], o[1], o[2], o[3]);
     }

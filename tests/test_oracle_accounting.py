@@ -66,3 +66,16 @@ def test_product_accounting_matches_the_oracle():
         o = dict(args)
         o["rows3"], o["rows4"] = o.pop("rows_loop3"), o.pop("rows_loop4")
         assert accounting.reference_layer_storage_bytes(**args) == OA.kivi_layer_storage_bytes(**o)
+
+
+def test_pack_bytes_hand_computed():
+    # one (b,h) row of two 64-token groups, loops 3/4 storing 40 and 10 rows:
+    # read 128 tokens x 4 loops x (K + V) x 256 B = 262144, + 128 tokens x 2 masked loops x 5 B
+    # per stored row 128 code bytes + 24 V metadata + 16 record = 168;
+    # per group and stream 128 channels x 12 B = 1536
+    rd, wr = accounting.pack_bytes([128], [[128], [128], [40], [10]], masked_tokens=256)
+    assert rd == 262144 + 1280
+    assert wr == (128 + 128 + 40 + 10) * 168 + 4 * 2 * 1536
+    # cfg3 unmasked: 128 rows of 32768 tokens -> 8.59 GB read, 3.22 GB written
+    rd, wr = accounting.pack_bytes([32768] * 128, [[32768] * 128] * 4)
+    assert rd == 8 * 128 * 32768 * 256 and wr == 4 * 128 * (32768 * 168 + 512 * 1536)
