@@ -806,30 +806,32 @@ def _assert_half_copies(layer, chain, tp, batch, heads):
     scale/min, at the documented layouts: K [bh, group, channel, (scale, min)], V
     [bh, row, half, (scale, min)], and the per-token record [bh, token, half, stream,
     (scale, min)] in fp32."""
-    bh = batch * heads
-    G = tp // 64
-    rec = layer.value_meta_token.cpu().numpy()
-    for s in range(4):
-        sc = chain.streams[s]
-        kh = layer.key_meta_half[s].cpu().numpy()
-        vh = layer.value_meta_half[s].cpu().numpy()
-        want_ks = sc.k_scale.reshape(bh, G, 128).astype(np.float16)
-        want_km = sc.k_min.reshape(bh, G, 128).astype(np.float16)
-        assert np.array_equal(kh[:, :G, :, 0].view(np.uint16), want_ks.view(np.uint16)), f"stream {s}: fp16 K scale"
-        assert np.array_equal(kh[:, :G, :, 1].view(np.uint16), want_km.view(np.uint16)), f"stream {s}: fp16 K min"
-        ovs = sc.v_scale.reshape(batch, heads, tp, 2)
-        ovm = sc.v_min.reshape(batch, heads, tp, 2)
-        for b in range(batch):
-            t_idx = np.nonzero(sc.active[b, :tp])[0]
-            rows = t_idx if s < 2 else layer.rank[s - 2][b].cpu().numpy()[t_idx]
-            for h in range(heads):
-                r = b * heads + h
-                for j, want in ((0, ovs), (1, ovm)):
-                    got16 = vh[r, rows, :, j].view(np.uint16)
-                    assert np.array_equal(got16, want[b, h, t_idx].astype(np.float16).view(np.uint16)), \
-                        f"stream {s}: fp16 V meta {j} (b={b}, h={h})"
-                    assert np.array_equal(rec[r, t_idx, :, s, j], want[b, h, t_idx]), \
-                        f"stream {s}: per-token V record {j} (b={b}, h={h})"
+    with np.errstate(over="ignore"):  # fp16 copies overflow to inf by design
+        bh = batch * heads
+        G = tp // 64
+        rec = layer.value_meta_token.cpu().numpy()
+        for s in range(4):
+            sc = chain.streams[s]
+            kh = layer.key_meta_half[s].cpu().numpy()
+            vh = layer.value_meta_half[s].cpu().numpy()
+            want_ks = sc.k_scale.reshape(bh, G, 128).astype(np.float16)
+            want_km = sc.k_min.reshape(bh, G, 128).astype(np.float16)
+            assert np.array_equal(kh[:, :G, :, 0].view(np.uint16), want_ks.view(np.uint16)), f"stream {s}: fp16 K scale"
+            assert np.array_equal(kh[:, :G, :, 1].view(np.uint16), want_km.view(np.uint16)), f"stream {s}: fp16 K min"
+            ovs = sc.v_scale.reshape(batch, heads, tp, 2)
+            ovm = sc.v_min.reshape(batch, heads, tp, 2)
+            for b in range(batch):
+                t_idx = np.nonzero(sc.active[b, :tp])[0]
+                rows = t_idx if s < 2 else layer.rank[s - 2][b].cpu().numpy()[t_idx]
+                for h in range(heads):
+                    r = b * heads + h
+                    for j, want in ((0, ovs), (1, ovm)):
+                        got16 = vh[r, rows, :, j].view(np.uint16)
+                        assert np.array_equal(got16, want[b, h, t_idx].astype(np.float16).view(np.uint16)), \
+                            f"stream {s}: fp16 V meta {j} (b={b}, h={h})"
+                        assert np.array_equal(rec[r, t_idx, :, s, j].view(np.uint32),
+                                              want[b, h, t_idx].view(np.uint32)), \
+                            f"stream {s}: per-token V record {j} (b={b}, h={h})"
 
 
 @pytest.mark.parametrize("masked", [False, True])

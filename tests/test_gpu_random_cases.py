@@ -1,9 +1,12 @@
 """Seeded random cases of the decode path against the oracle: whole decode steps, decode
-appends across rollovers, and the decode top-k on adversarial score rows.  Each case draws
+appends across rollovers, the decode top-k on adversarial score rows, and the pack
+kernel on adversarial value distributions.  Each case draws
 its shape, lengths, masks and retention from its seed (printed first), then holds the
 results to the same bars as the fixed-shape parity tests."""
 
 from __future__ import annotations
+
+import math
 
 import numpy as np
 import pytest
@@ -151,3 +154,62 @@ def test_random_topk_rows(seed):
     fw = np.isfinite(sel.selected_weights)
     assert np.allclose(gw[fw], sel.selected_weights[fw], rtol=2e-5, atol=1e-8), "weights differ"
     assert nf.cpu().tolist() == [int(np.sum(np.isnan(x) | np.isinf(x))) for x in row_list], "non-finite counts"
+
+
+def _draw(shape, kind, g):
+    if kind == "cauchy":
+        x = torch.tan(math.pi * (torch.rand(shape, generator=g) - 0.5)).clamp(-3e38, 3e38)  # standard Cauchy
+    elif kind == "uniform":
+        x = torch.rand(shape, generator=g) * 2 - 1
+    elif kind == "scaled":  # per-head magnitudes from 1e-30 to 1e30
+        x = torch.randn(shape, generator=g) * (10.0 ** torch.randint(-30, 30, (shape[0], shape[1], 1, 1),
+                                                                        generator=g).float())
+    elif kind == "constant":  # near-constant channels: tiny spans
+        x = torch.randn(shape[:-1] + (1,), generator=g).expand(shape).clone()
+        x[..., ::7] += 1e-3
+    elif kind == "sparse":  # 95% zeros, signed (-0.0 from negative draws)
+        x = torch.randn(shape, generator=g) * (torch.rand(shape, generator=g) < 0.05)
+    elif kind == "quantized":  # half-integers: exact ties in the quotient
+        x = torch.randint(-8, 8, shape, generator=g).float() * 0.5
+    else:
+        x = torch.randn(shape, generator=g)
+    return x
+
+
+@pytest.mark.parametrize("seed", range(14))
+def test_random_pack(seed):
+    """The pack kernel on 1-2 sequences x 1-3 heads x 64-700 tokens drawn Cauchy, uniform,
+    scaled by 10^+-30, near-constant, 95%-sparse (signed zeros), half-integer or normal,
+    with per-loop drift 0-10x, masked or not: codes, fp32 and fp16 metadata and the bf16
+    reconstructions equal the oracle's bit for bit (bit patterns, so zero signs count)."""
+    rng = np.random.default_rng(4000 + seed)
+    B, H, T = int(rng.integers(1, 3)), int(rng.integers(1, 4)), int(rng.integers(64, 700))
+    kind = ["cauchy", "uniform", "scaled", "constant", "sparse", "quantized", "normal"][seed % 7]
+    drift = float(rng.choice([0.0, 1e-3, 0.1, 1.0, 10.0]))
+    masked = bool(rng.random() < 0.5)
+    print(f"case: random pack seed={seed} B{B} H{H} T{T} kind={kind} drift={drift} masked={masked}", flush=True)
+    g = torch.Generator().manual_seed(5000 + seed)
+    shape = (B, H, T, 128)
+    k, v = _draw(shape, kind, g), _draw(shape, kind, g)
+    ks, vs = [], []
+    for r in range(4):
+        ks.append(k.bfloat16())
+        vs.append(v.bfloat16())
+        k = k.float() + drift * _draw(shape, kind, g)
+        v = v.float() + drift * _draw(shape, kind, g)
+    m3 = m4 = None
+    kw = {}
+    if masked:
+        m3, m4 = P._masks(B, T, seed, p3=float(rng.uniform(0.1, 0.9)), p4=float(rng.uniform(0.1, 0.9)))
+        kw = dict(mask_loop3=torch.from_numpy(m3).to(DEV), mask_loop4=torch.from_numpy(m4).to(DEV))
+    layer = CrossLoopKVLayer.from_prefill([x.to(DEV) for x in ks], [x.to(DEV) for x in vs], recon=True, **kw)
+    torch.cuda.synchronize()
+    _, _, chain, tp = oracle_prefix(ks, vs, m3, m4)
+    assert tp == layer.quantized_tokens
+    assert_layer_matches_chain(layer, chain, tp, B, H)
+    for r in range(4 if tp else 0):  # (below 128 tokens nothing is packed)
+        gk = np32(layer.recon_keys[r]).reshape(B, H, T, 128)[:, :, :tp]
+        gv = np32(layer.recon_values[r]).reshape(B, H, T, 128)[:, :, :tp]
+        assert np.array_equal(gk.view(np.uint32), chain.recon_keys[r].view(np.uint32)), f"R_{r} keys differ"
+        assert np.array_equal(gv.view(np.uint32), chain.recon_values[r].view(np.uint32)), f"R_{r} values differ"
+    P._assert_half_copies(layer, chain, tp, B, H)
